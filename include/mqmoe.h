@@ -1,0 +1,222 @@
+/*
+ * mqmoe.h -- C ABI of the MI355X (gfx950) Flash-Next quantized MoE expert path.
+ *
+ * Every pointer argument is a caller-owned device pointer unless stated
+ * otherwise; every size is in elements unless it says bytes.  Streams and
+ * events are passed as opaque pointers (hipStream_t / hipEvent_t; NULL is the
+ * default stream).  Functions return 0 on success and a negative MQ_ERR_*
+ * code on failure; the message of the last failure on the calling thread is
+ * available from mq_last_error().  No function throws across the ABI.
+ *
+ * Weights use the reference's affine Q4 format: uint32 words holding eight
+ * 4-bit values LSB first (value k of a row in word k>>3, bits 4*(k&7)), with
+ * bf16 scales and biases per group of `group_size` inputs, w = s*q + b.
+ * Activations ("T") are bf16 (MQ_BF16) or float32 (MQ_F32).
+ */
+#ifndef MQMOE_H
+#define MQMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MQ_OK 0
+#define MQ_ERR_INVALID (-1)     /* bad argument, shape or bound */
+#define MQ_ERR_DEVICE (-2)      /* no usable gfx950 device */
+#define MQ_ERR_LAUNCH (-3)      /* a HIP call or kernel launch failed */
+#define MQ_ERR_UNSUPPORTED (-4) /* valid request this build does not implement */
+#define MQ_ERR_TIMEOUT (-5)     /* a bounded in-kernel wait expired */
+#define MQ_ERR_NOMEM (-6)       /* library workspace allocation failed */
+
+#define MQ_F32 0
+#define MQ_BF16 1
+
+#define MQ_SLOT_BIT 0x80000000u /* route word: bit 31 set = pool slot */
+
+/* Bounds of the decode executor (models/flashnext/metal_runtime.py:26-31). */
+#define MQ_MAX_TOKENS 8
+#define MQ_MAX_EXPERTS 512
+#define MQ_MAX_TOP_K 10
+#define MQ_MAX_WIDTH 16384
+
+/*
+ * One projection (gate, up or down) of an expert bank.  A route word with
+ * MQ_SLOT_BIT set addresses a record in `pool`:
+ *   base = pool + pool_header + (uint64)(word & 0x7FFFFFFF) * pool_stride
+ *   weight = base + off_weight, scales = base + off_scales, biases = base + off_biases
+ * (models/flashnext/metal_runtime.py:194-228).  Any other word indexes the
+ * expert-major record pack `stream_pack` when it is set (same record layout,
+ * no header: base = stream_pack + word * pool_stride), else the dense arrays
+ * weight [E, out, in/8], scales/biases [E, out, in/group].
+ */
+typedef struct MqProjection {
+  const uint32_t *weight;
+  const uint16_t *scales;
+  const uint16_t *biases;
+  const uint8_t *pool;
+  uint64_t pool_header;
+  uint64_t pool_stride;
+  uint64_t off_weight;
+  uint64_t off_scales;
+  uint64_t off_biases;
+  const uint8_t *stream_pack;
+} MqProjection;
+
+/* Arguments of mq_moe_decode: the fields of the reference's native bridge
+ * struct FlashNextMoEArgs (tests/bench/metal_runtime_native.mm:175-194) plus
+ * the pool, score combine and shared-expert epilogues of
+ * MetalMoEExecutor.execute (models/flashnext/metal_runtime.py:764-932). */
+typedef struct MqMoeArgs {
+  const void *x;          /* [tokens, hidden] T */
+  int x_dtype;            /* MQ_BF16 or MQ_F32; outputs use the same T */
+  MqProjection gate;      /* [E, inter, hidden/8] */
+  MqProjection up;        /* [E, inter, hidden/8] */
+  MqProjection down;      /* [E, hidden, inter/8] */
+  const uint32_t *routes; /* [tokens, slots] route words */
+  const void *scores;     /* [tokens, slots] or NULL (then return_all must be 1) */
+  int score_dtype;        /* MQ_F32 or MQ_BF16 */
+  const int32_t *keeps;   /* [tokens] active slot prefix per token, or NULL (= slots) */
+  /* shared epilogue: at most one of shared_y / (shared, shared_gate) / shared expert */
+  const void *shared_y;      /* [tokens, hidden] T: out = T(T(acc) + shared_y) */
+  const void *shared;        /* [tokens, hidden] T: out = T(T(acc) + T(shared*gate)) */
+  const uint16_t *shared_gate; /* [tokens] bf16 sigmoid gate (with `shared` or shared expert) */
+  const MqProjection *shared_expert; /* NULL or a HOST array of 3 projections {gate, up, down}
+                                        of one expert (route word 0), read during the call;
+                                        computed in-kernel and combined like `shared` with
+                                        `shared_gate` */
+  void *out;              /* [tokens, hidden] T (combined) */
+  void *gate_out;         /* optional [tokens, slots, inter] T (return_all diagnostics) */
+  void *up_out;           /* optional [tokens, slots, inter] T */
+  void *act_out;          /* optional [tokens, slots(+1 with shared expert), inter] T */
+  void *down_out;         /* optional [tokens, slots, hidden] T, per-slot down (return_all) */
+  uint32_t tokens;
+  uint32_t slots;
+  uint32_t hidden;
+  uint32_t inter;
+  uint32_t expert_count;
+  uint32_t group_size;    /* 32 or 64 */
+  uint32_t flags;         /* MQ_DECODE_* */
+} MqMoeArgs;
+
+#define MQ_DECODE_RETURN_ALL 1u    /* write gate_out/up_out/act_out/down_out, skip combine */
+#define MQ_DECODE_UNFUSED_UP 2u    /* separate up projection + SwiGLU pass (bit-identical) */
+
+/* Arguments of mq_route_topk: the router chain of _moe_call
+ * (models/flashnext/adaptive_topk.py:53-64, 75-261; compiled.py:61-71) and
+ * the slot lookup of StreamingSwitchGLU._pool_pass
+ * (models/flashnext/expert_cache.py:1694-1725). */
+typedef struct MqRouteArgs {
+  const uint16_t *x;        /* [tokens, hidden] bf16 */
+  const uint16_t *gate_w;   /* [experts, hidden] bf16 router gate, or NULL when logits_in */
+  const uint16_t *logits_in;/* [tokens, experts] bf16 precomputed logits, or NULL */
+  const uint16_t *shared_gate_w; /* [hidden] bf16 shared-expert gate row, or NULL */
+  const uint32_t *slot_table;    /* [experts] pool slot per expert, or NULL (routes = expert ids) */
+  uint16_t *logits_out;     /* optional [tokens, experts] bf16 */
+  uint32_t *inds;           /* [tokens, top_k] expert ids, score-descending, ties by index */
+  void *scores;             /* [tokens, top_k] renormalised scores */
+  int score_dtype;          /* MQ_BF16 (bf16 arithmetic result) or MQ_F32 (widened) */
+  uint16_t *scores_raw;     /* optional [tokens, top_k] bf16 softmax gates before renorm */
+  uint32_t *routes;         /* optional [tokens, top_k] route words */
+  int32_t *keeps;           /* optional [tokens] adaptive keep count */
+  uint16_t *shared_gate;    /* optional [tokens] bf16 sigmoid(x . shared_gate_w) */
+  uint32_t tokens;
+  uint32_t hidden;
+  uint32_t experts;
+  uint32_t top_k;
+  float threshold;          /* >= 1: keep all top_k; < 1: adaptive keep + pad */
+  uint32_t min_keep;
+  float blend;              /* renorm blend (1 = divide by selected mass) */
+} MqRouteArgs;
+
+/* Arguments of mq_moe_grouped: the >8-token (prefill / verify) path of
+ * StreamingSwitchGLU._one_pass/_issue (models/flashnext/expert_cache.py:1743-1810):
+ * gather_qmm gate/up -> SwiGLU -> gather_qmm down with token sorting, then
+ * the bf16 generic combine (models/flashnext/adaptive_topk.py:274-277). */
+typedef struct MqGroupedArgs {
+  const uint16_t *x;        /* [tokens, hidden] bf16 */
+  MqProjection gate, up, down;
+  const uint32_t *routes;   /* [tokens, slots] route words */
+  const uint16_t *scores;   /* [tokens, slots] bf16, or NULL (then only y is written) */
+  const uint16_t *shared;   /* optional [tokens, hidden] bf16 */
+  const uint16_t *shared_gate; /* optional [tokens] bf16 */
+  uint16_t *out;            /* [tokens, hidden] bf16 combined, or NULL */
+  uint16_t *y;              /* optional [tokens, slots, hidden] bf16 per-slot outputs */
+  void *workspace;          /* device scratch of mq_grouped_workspace_size() bytes */
+  uint64_t workspace_bytes;
+  uint32_t tokens, slots, hidden, inter, expert_count, group_size;
+} MqGroupedArgs;
+
+/* ---- capability and errors (tests/bench/metal_runtime_native.mm:196-205) ---- */
+
+/* 1 when a gfx950 device is usable from this process, else 0. */
+int mq_available(void);
+
+/* Copy the calling thread's last error message into buf (NUL-terminated). */
+int mq_last_error(char *buf, uint32_t max_len);
+
+/* Library version as major*10000 + minor*100 + patch. */
+int mq_version(void);
+
+/* ---- record layout (models/flashnext/slab_pack.py:96-149) ---- */
+
+/* Byte offsets of the nine parts (gate/up/down x weight/scales/biases) and the
+ * page-aligned record stride for a (hidden, inter, group) expert. */
+int mq_record_layout(uint32_t hidden, uint32_t inter, uint32_t group_size,
+                     uint64_t offsets[9], uint64_t *stride);
+
+/* ---- Q4 primitives ---- */
+
+/* Unpack n_words packed words into 8*n_words uint8 values (metal_runtime.py:980). */
+int mq_q4_unpack(const uint32_t *words, uint8_t *values, uint64_t n_words, void *stream);
+
+/* bf16(s*q + b) for a [rows, cols] Q4 matrix (mx.dequantize semantics). */
+int mq_q4_dequant(const uint32_t *weight, const uint16_t *scales, const uint16_t *biases,
+                  uint16_t *out, uint32_t rows, uint32_t cols, uint32_t group_size,
+                  void *stream);
+
+/* y[m, n] = T(sum_k x[m, k] * (s*q + b)[n, k]) for m < rows_x:
+ * mx.quantized_matmul(x, w, s, b, transpose=True, group_size, bits=4) as
+ * reached through nn.QuantizedLinear (models/flashnext/loader.py:190-217).
+ * x and y share dtype x_dtype. */
+int mq_q4_qmv(const void *x, int x_dtype, const uint32_t *weight, const uint16_t *scales,
+              const uint16_t *biases, void *y, uint32_t rows_x, uint32_t out_features,
+              uint32_t in_features, uint32_t group_size, void *stream);
+
+/* out[t, s, :] = T(W_{route[t,s]} . x[t or (t,s)]): the per-projection QMV of
+ * MetalMoEExecutor._metal_projection (models/flashnext/metal_runtime.py:640-667)
+ * and mx.gather_qmm for decode shapes (models/flashnext/expert_cache.py:799-810).
+ * slot_input != 0 reads x as [tokens, slots, in]. */
+int mq_gather_qmv(const void *x, int x_dtype, int slot_input, const MqProjection *proj,
+                  const uint32_t *routes, void *out, uint32_t tokens, uint32_t slots,
+                  uint32_t in_features, uint32_t out_features, uint32_t expert_count,
+                  uint32_t group_size, void *stream);
+
+/* ---- router ---- */
+int mq_route_topk(const MqRouteArgs *args, void *stream);
+
+/* ---- decode executor (MetalMoEExecutor.execute, metal_runtime.py:764-932) ---- */
+int mq_moe_decode(const MqMoeArgs *args, void *stream);
+
+/* ---- prefill / verify grouped path ---- */
+uint64_t mq_grouped_workspace_size(uint32_t tokens, uint32_t slots, uint32_t hidden,
+                                   uint32_t inter, uint32_t expert_count);
+int mq_moe_grouped(const MqGroupedArgs *args, void *stream);
+
+/* ---- expert slot pool refill (models/flashnext/expert_pool.py:112-145) ----
+ * Copy n records of record_bytes each from pinned host memory to pool slots
+ * on copy_stream, then record done_event (if not NULL) on that stream.
+ * `slots` and `host_records` are HOST arrays of n entries; each
+ * host_records[i] must be host-pinned memory (hipHostMalloc). */
+int mq_pool_refill_async(uint8_t *pool, uint64_t pool_header, uint64_t pool_stride,
+                         const uint32_t *slots, const void *const *host_records,
+                         uint32_t n, uint64_t record_bytes, void *copy_stream,
+                         void *done_event);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MQMOE_H */

@@ -1,0 +1,191 @@
+// Internal helpers shared by the gfx950 kernels of the quantized MoE path.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mqmoe.h"
+
+namespace mq {
+
+// ---------------------------------------------------------------- errors
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int hip_fail(hipError_t err, const char *what);
+int check_launch(const char *what);
+#define MQ_TRY_HIP(expr)                                  \
+  do {                                                    \
+    hipError_t _e = (expr);                               \
+    if (_e != hipSuccess) return ::mq::hip_fail(_e, #expr); \
+  } while (0)
+
+// Per-device library workspace (counters, error flags).  Allocated once per
+// device on first use and zeroed; kernels restore every counter they use.
+struct DeviceWorkspace {
+  unsigned int *counters;  // kCounterSlots arrival counters
+  unsigned int *flags;     // error flags set by bounded waits
+};
+constexpr int kCounterSlots = 64;
+int workspace(DeviceWorkspace **out);
+
+// ---------------------------------------------------------------- bf16
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even float -> bf16; NaN -> quiet NaN with the sign kept.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>(((u >> 16) & 0x8000u) | 0x7fc0u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+
+// Activation type traits: T storage and "one T-typed operation" rounding.
+struct BF16T {
+  using storage = uint16_t;
+  static constexpr int dtype = MQ_BF16;
+  __device__ static __forceinline__ float load(storage v) { return bf16_to_f32(v); }
+  __device__ static __forceinline__ storage store(float f) { return f32_to_bf16(f); }
+  __device__ static __forceinline__ float round(float f) { return round_bf16(f); }
+};
+struct F32T {
+  using storage = float;
+  static constexpr int dtype = MQ_F32;
+  __device__ static __forceinline__ float load(storage v) { return v; }
+  __device__ static __forceinline__ storage store(float f) { return f; }
+  __device__ static __forceinline__ float round(float f) { return f; }
+};
+
+// ---------------------------------------------------------------- packed bf16 math
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// acc + a.lo*b.lo + a.hi*b.hi with bf16 pairs packed in 32-bit words.
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
+
+// Nibbles k and k+4 of word w (k = 0..3) as the bf16 pair (128+q_k, 128+q_{k+4}).
+// 0x4300 is bf16 128.0 whose 7 mantissa bits count in units of 1.
+template <int K>
+__device__ __forceinline__ uint32_t nib_pair(uint32_t w) {
+  return ((w >> (4 * K)) & 0x000f000fu) | 0x43004300u;
+}
+
+// Activation chunk of 32 inputs held as 16 bf16 pairs matching nib_pair order:
+// for word j (inputs 8j..8j+7): p[4j+k] = (x[8j+k], x[8j+k+4]).
+struct XChunk {
+  uint32_t p[16];
+  float osum;  // sum of the 32 bf16 values held in p (removes the 128 offset)
+};
+
+// Build the pair layout from 4 consecutive uint32 (8 bf16 values).
+__device__ __forceinline__ void pairs_from_words(const uint32_t u[4], uint32_t *p) {
+  // u0 = (x0,x1) u1 = (x2,x3) u2 = (x4,x5) u3 = (x6,x7), low half first.
+  p[0] = __builtin_amdgcn_perm(u[2], u[0], 0x05040100u);  // (x0, x4)
+  p[1] = __builtin_amdgcn_perm(u[2], u[0], 0x07060302u);  // (x1, x5)
+  p[2] = __builtin_amdgcn_perm(u[3], u[1], 0x05040100u);  // (x2, x6)
+  p[3] = __builtin_amdgcn_perm(u[3], u[1], 0x07060302u);  // (x3, x7)
+}
+
+// Dot of one packed Q4 chunk (4 words = 32 nibbles) with an activation chunk:
+// returns sum_i x_i * q_i using the 128-offset pairs (the offset is removed
+// with the chunk sum).
+__device__ __forceinline__ float q4_chunk_dot(const uint4 &w, const XChunk &x) {
+  float d = 0.0f;
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    d = dot2_bf16(x.p[4 * j + 0], nib_pair<0>(ws[j]), d);
+    d = dot2_bf16(x.p[4 * j + 1], nib_pair<1>(ws[j]), d);
+    d = dot2_bf16(x.p[4 * j + 2], nib_pair<2>(ws[j]), d);
+    d = dot2_bf16(x.p[4 * j + 3], nib_pair<3>(ws[j]), d);
+  }
+  return d - 128.0f * x.osum;
+}
+
+// Sum of the 16 pairs (32 bf16 values) of a chunk.
+__device__ __forceinline__ float chunk_pair_sum(const XChunk &x) {
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) s = dot2_bf16(x.p[i], 0x3f803f80u, s);
+  return s;
+}
+
+// ---------------------------------------------------------------- DPP reductions
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over each 16-lane DPP row; every lane of the row receives a row sum.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x124>(v);  // row_ror:4
+  v += dpp_f<0x128>(v);  // row_ror:8
+  return v;
+}
+
+// Full 64-lane sum, uniform result (read through lane 0 of each DPP row).
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+  float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+  float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+  float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  for (int off = 32; off > 0; off >>= 1) {
+    uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64));
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------- expert addressing
+struct ExpertPtrs {
+  const uint32_t *w;
+  const uint16_t *s;
+  const uint16_t *b;
+};
+
+// Resolve a route word to the rows of one projection
+// (models/flashnext/metal_runtime.py:194-228; 64-bit pool offsets).
+__device__ __forceinline__ ExpertPtrs expert_ptrs(const MqProjection &p, uint32_t word,
+                                                  uint32_t out_w, uint32_t in_w,
+                                                  uint32_t group) {
+  ExpertPtrs r;
+  if (word & MQ_SLOT_BIT) {
+    const uint8_t *rec = p.pool + p.pool_header +
+                         static_cast<uint64_t>(word & 0x7fffffffu) * p.pool_stride;
+    r.w = reinterpret_cast<const uint32_t *>(rec + p.off_weight);
+    r.s = reinterpret_cast<const uint16_t *>(rec + p.off_scales);
+    r.b = reinterpret_cast<const uint16_t *>(rec + p.off_biases);
+  } else if (p.stream_pack != nullptr) {
+    const uint8_t *rec = p.stream_pack + static_cast<uint64_t>(word) * p.pool_stride;
+    r.w = reinterpret_cast<const uint32_t *>(rec + p.off_weight);
+    r.s = reinterpret_cast<const uint16_t *>(rec + p.off_scales);
+    r.b = reinterpret_cast<const uint16_t *>(rec + p.off_biases);
+  } else {
+    const uint64_t e = word;
+    r.w = p.weight + e * out_w * (in_w / 8);
+    r.s = p.scales + e * out_w * (in_w / group);
+    r.b = p.biases + e * out_w * (in_w / group);
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------- host helpers
+inline uint32_t ceil_div(uint64_t a, uint64_t b) { return static_cast<uint32_t>((a + b - 1) / b); }
+
+}  // namespace mq

@@ -1,0 +1,115 @@
+"""The MoE block composition of ``_moe_call`` on gfx950.
+
+``_moe_call`` (``models/flashnext/adaptive_topk.py:53-292``) runs the router,
+renormalises, computes the shared expert and its sigmoid gate, then hands the
+routed experts, scores and ``shared_y`` to the switch block whose executor
+fuses the combine.  :class:`DecodeLayer` does the same with two C-ABI calls
+into device-resident buffers (router kernel pair, then the fused expert
+kernels with the shared expert in-kernel), so one decode step needs no host
+synchronisation and can be captured in a HIP graph.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._tensors import ptr
+from .layout import HEADER_SIZE, SlabLayout
+from .ops import dense_projection
+
+
+def pool_projection(pool: torch.Tensor, layout: SlabLayout, name: str) -> _lib.MqProjection:
+    p = _lib.MqProjection()
+    p.pool = ptr(pool)
+    p.pool_header = HEADER_SIZE
+    p.pool_stride = layout.record_stride
+    p.off_weight = layout.offset(name, "weight")
+    p.off_scales = layout.offset(name, "scales")
+    p.off_biases = layout.offset(name, "biases")
+    return p
+
+
+@dataclass
+class LayerWeights:
+    """Device-resident weights of one MoE layer addressed through a slot pool."""
+
+    layout: SlabLayout
+    pool: torch.Tensor
+    slot_table: torch.Tensor
+    router_w: torch.Tensor
+    shared_gate_w: torch.Tensor | None
+    shared: tuple | None  # three (weight, scales, biases) dense single-expert banks
+
+
+class DecodeLayer:
+    """One MoE decode layer for a fixed token count, with preallocated buffers."""
+
+    def __init__(self, weights: LayerWeights, tokens: int, top_k: int, *, threshold: float = 1.0,
+                 min_keep: int = 1, blend: float = 1.0, device="cuda"):
+        lay = weights.layout
+        self.w = weights
+        self.tokens, self.top_k = tokens, top_k
+        self.hidden, self.inter = lay.hidden, lay.inter
+        self.experts = weights.router_w.shape[0]
+        dev = torch.device(device)
+        bf = torch.bfloat16
+        self.x = torch.zeros((tokens, self.hidden), dtype=bf, device=dev)
+        self.logits = torch.empty((tokens, self.experts), dtype=bf, device=dev)
+        self.inds = torch.empty((tokens, top_k), dtype=torch.int32, device=dev)
+        self.scores = torch.empty((tokens, top_k), dtype=bf, device=dev)
+        self.scores_raw = torch.empty((tokens, top_k), dtype=bf, device=dev)
+        self.routes = torch.empty((tokens, top_k), dtype=torch.int32, device=dev)
+        self.keeps = torch.empty((tokens,), dtype=torch.int32, device=dev)
+        self.shared_gate = torch.empty((tokens,), dtype=bf, device=dev)
+        has_shared = weights.shared is not None
+        self.act = torch.empty((tokens * top_k + (tokens if has_shared else 0), self.inter), dtype=bf, device=dev)
+        self.out = torch.empty((tokens, self.hidden), dtype=bf, device=dev)
+
+        r = _lib.MqRouteArgs()
+        r.x, r.gate_w, r.logits_in = ptr(self.x), ptr(weights.router_w), None
+        r.shared_gate_w = ptr(weights.shared_gate_w) if has_shared else None
+        r.slot_table = ptr(weights.slot_table)
+        r.logits_out = ptr(self.logits)
+        r.inds, r.scores, r.score_dtype = ptr(self.inds), ptr(self.scores), _lib.MQ_BF16
+        r.scores_raw, r.routes, r.keeps = ptr(self.scores_raw), ptr(self.routes), ptr(self.keeps)
+        r.shared_gate = ptr(self.shared_gate) if has_shared else None
+        r.tokens, r.hidden, r.experts, r.top_k = tokens, self.hidden, self.experts, top_k
+        r.threshold, r.min_keep, r.blend = float(threshold), int(min_keep), float(blend)
+        self.route_args = r
+
+        a = _lib.MqMoeArgs()
+        a.x, a.x_dtype = ptr(self.x), _lib.MQ_BF16
+        a.gate = pool_projection(weights.pool, lay, "gate_proj")
+        a.up = pool_projection(weights.pool, lay, "up_proj")
+        a.down = pool_projection(weights.pool, lay, "down_proj")
+        a.routes, a.scores, a.score_dtype = ptr(self.routes), ptr(self.scores), _lib.MQ_BF16
+        a.keeps = ptr(self.keeps) if threshold < 1.0 else None
+        if has_shared:
+            self._shared_projs = (_lib.MqProjection * 3)(*[dense_projection(*bank) for bank in weights.shared])
+            import ctypes
+
+            a.shared_expert = ctypes.addressof(self._shared_projs)
+            a.shared_gate = ptr(self.shared_gate)
+        a.out, a.act_out = ptr(self.out), ptr(self.act)
+        a.tokens, a.slots, a.hidden, a.inter = tokens, top_k, self.hidden, self.inter
+        a.expert_count, a.group_size = self.experts, lay.group_size
+        self.moe_args = a
+        self._lib = _lib.load()
+
+    def launch(self, stream: int | None) -> None:
+        """Route + experts on ``stream`` (a raw hipStream_t handle)."""
+        lib = self._lib
+        rc = lib.mq_route_topk(self.route_args, stream)
+        if rc:
+            _lib.check(rc, lib)
+        rc = lib.mq_moe_decode(self.moe_args, stream)
+        if rc:
+            _lib.check(rc, lib)
+
+    def launch_router(self, stream):
+        _lib.check(self._lib.mq_route_topk(self.route_args, stream), self._lib)
+
+    def launch_experts(self, stream):
+        _lib.check(self._lib.mq_moe_decode(self.moe_args, stream), self._lib)

@@ -1,0 +1,104 @@
+"""Shared helpers for the parity tests: seeded synthetic banks and tolerances.
+
+Synthetic inputs follow the benchmark description: activations ~N(0,1),
+weights ~N(0,0.02) quantised to affine Q4 with group 32, bf16 metadata.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+
+from oracle import bf16, q4
+
+# Value tolerance for bf16 layer outputs (max rel err <= 1e-2
+# and cosine >= 0.9999; the reference's own tests use rtol 2e-2 / atol 3e-3).
+RTOL = 1e-2
+ATOL = 3e-3
+MIN_COSINE = 0.9999
+MAX_REL = 1e-2
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def make_bank(experts: int, out_w: int, in_w: int, seed: int, group: int = 32, std: float = 0.02):
+    rng = np.random.default_rng(seed)
+    w = rng.normal(0.0, std, (experts, out_w, in_w)).astype(np.float32)
+    packed, scales, biases = q4.quantize_affine(w, group)
+    return q4.ExpertBank(packed, scales, biases, group)
+
+
+def make_records(experts: int, hidden: int, inter: int, seed: int, group: int = 32):
+    from oracle.moe import ExpertRecordSet
+
+    return ExpertRecordSet(
+        make_bank(experts, inter, hidden, seed + 1, group),
+        make_bank(experts, inter, hidden, seed + 2, group),
+        make_bank(experts, hidden, inter, seed + 3, group),
+    )
+
+
+def bf16_normal(shape, seed: int, std: float = 1.0) -> np.ndarray:
+    rng = np.random.default_rng(seed)
+    return bf16.f32_to_bf16(rng.normal(0.0, std, shape).astype(np.float32))
+
+
+def to_dev_bank(bank, device="cuda"):
+    import torch
+
+    return (torch.from_numpy(bank.packed.view(np.int32)).to(device),
+            torch.from_numpy(bank.scales.view(np.int16)).to(device).view(torch.bfloat16),
+            torch.from_numpy(bank.biases.view(np.int16)).to(device).view(torch.bfloat16))
+
+
+def to_dev_bf16(bits, device="cuda"):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(device).view(torch.bfloat16)
+
+
+def from_dev_bf16(t) -> np.ndarray:
+    import torch
+
+    return t.detach().contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def value_report(actual: np.ndarray, expected: np.ndarray) -> dict:
+    a = np.asarray(actual, dtype=np.float64)
+    e = np.asarray(expected, dtype=np.float64)
+    delta = np.abs(a - e)
+    scale = float(np.abs(e).max()) if e.size else 0.0
+    cos = float(np.sum(a * e) / (np.linalg.norm(a) * np.linalg.norm(e))) if scale > 0 else 1.0
+    return {"max_abs": float(delta.max()) if delta.size else 0.0,
+            "max_rel": float(delta.max() / scale) if scale > 0 else 0.0,
+            "cosine": cos}
+
+
+def assert_close(actual, expected, msg: str, rtol=RTOL, atol=ATOL, min_cos=MIN_COSINE, max_rel=MAX_REL):
+    rep = value_report(actual, expected)
+    np.testing.assert_allclose(np.asarray(actual, np.float64), np.asarray(expected, np.float64),
+                               rtol=rtol, atol=atol, err_msg=f"{msg}: {rep}")
+    assert rep["cosine"] >= min_cos, f"{msg}: cosine {rep['cosine']:.8f} < {min_cos}"
+    assert rep["max_rel"] <= max_rel, f"{msg}: max_rel {rep['max_rel']:.3g} > {max_rel}"
+    return rep
+
+
+def pool_from_banks(records, slot_of_expert, slots: int, hidden: int, inter: int, group: int = 32):
+    """Build a pool image (header + slots*stride bytes) holding each expert's
+    record at its slot, parts at the layout offsets."""
+    from oracle import pool as opool
+
+    offs, stride, sizes = opool.record_layout(hidden, inter, group)
+    img = np.zeros(opool.HEADER + slots * stride, dtype=np.uint8)
+    banks = {"gate_proj": records.gate, "up_proj": records.up, "down_proj": records.down}
+    for e, slot in enumerate(slot_of_expert):
+        base = opool.HEADER + int(slot) * stride
+        for proj, bank in banks.items():
+            for part, arr in (("weight", bank.packed), ("scales", bank.scales), ("biases", bank.biases)):
+                payload = np.ascontiguousarray(arr[e]).view(np.uint8).reshape(-1)
+                start = base + offs[f"{proj}.{part}"]
+                img[start:start + payload.size] = payload
+    return img, stride

@@ -1,0 +1,73 @@
+"""C-ABI surface checks that need no GPU: load, exports, layout, error paths."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from flashnext_hip import _lib, layout
+from oracle import pool
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "mqmoe.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^(?:int|uint64_t)\s+(mq_\w+)\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    names = declared_functions()
+    assert names, "header parse found no declarations"
+    for name in names:
+        assert hasattr(lib, name), f"{name} missing from libmqmoe.so"
+    assert set(names) == set(_lib.EXPORTS)
+
+
+def test_version_and_last_error_round_trip():
+    lib = _lib.load()
+    assert lib.mq_version() >= 100
+    # Invalid arguments are rejected before any device call.
+    assert lib.mq_route_topk(None, None) == _lib.MQ_ERR_INVALID
+    assert "NULL" in _lib.last_error(lib)
+    assert lib.mq_moe_decode(None, None) == _lib.MQ_ERR_INVALID
+    buf = ctypes.create_string_buffer(4)
+    assert lib.mq_last_error(buf, 4) == 0 and len(buf.value) <= 3
+
+
+@pytest.mark.parametrize("hidden,inter,group", [(2560, 640, 32), (2560, 640, 64), (2048, 512, 32),
+                                                (1024, 256, 64), (4096, 1536, 32)])
+def test_record_layout_c_python_oracle_agree(hidden, inter, group):
+    offs_c, stride_c = _lib.record_layout(hidden, inter, group)
+    lay = layout.make_layout(hidden, inter, group)
+    offs_o, stride_o, _ = pool.record_layout(hidden, inter, group)
+    keys = [f"{p}.{q}" for p, q in layout.PART_KEYS]
+    assert stride_c == lay.record_stride == stride_o
+    assert offs_c == [lay.offset(*k) for k in layout.PART_KEYS] == [offs_o[k] for k in keys]
+
+
+def test_record_layout_rejects_bad_shapes():
+    with pytest.raises(ValueError):
+        _lib.record_layout(2048, 500, 32)
+    with pytest.raises(ValueError):
+        _lib.record_layout(2048, 512, 16)
+
+
+def test_validation_errors_without_device():
+    lib = _lib.load()
+    args = _lib.MqRouteArgs()
+    args.tokens, args.experts, args.top_k = 1, 512, 11
+    assert lib.mq_route_topk(args, None) == _lib.MQ_ERR_INVALID  # no outputs
+    args.experts, args.top_k = 600, 10
+    assert lib.mq_route_topk(args, None) == _lib.MQ_ERR_INVALID
+    assert "experts" in _lib.last_error(lib)
+    assert lib.mq_q4_dequant(None, None, None, None, 1, 32, 32, None) == _lib.MQ_ERR_INVALID
+    assert lib.mq_q4_unpack(None, None, 0, None) == _lib.MQ_OK  # empty is a no-op
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(_lib.NativeUnavailable):
+        _lib.load(tmp_path / "missing.so")
