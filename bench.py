@@ -60,15 +60,17 @@ def build_layers(n_layers: int, device, seed: int = 1234):
 
 
 def time_graph(torch, graph, replays: int, stream) -> float:
+    """Milliseconds for `replays` launches of `graph` on `stream` (events on the same stream)."""
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    start.record(stream)
-    for _ in range(replays):
-        graph.replay()
-    end.record(stream)
+    with torch.cuda.stream(stream):  # CUDAGraph.replay() launches on the current stream
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        end.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(end)  # ms
+    return start.elapsed_time(end)
 
 
 def capture(torch, fn, stream):
@@ -175,16 +177,21 @@ def main() -> int:
     gen.manual_seed(99)
     for r in runners:
         r.x.copy_(torch.randn(r.x.shape, generator=gen, device=dev).to(torch.bfloat16))
+    # The weights, slot tables and tokens were written on the default stream;
+    # the side stream below must not start before they are complete.
+    torch.cuda.synchronize()
     stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
     handle = stream.cuda_stream
     with torch.cuda.stream(stream):
         for r in runners:  # eager pass allocates library scratch before capture
             r.launch(handle)
+    _lib.check_device_errors(handle)  # raises if any route word was out of range
     torch.cuda.synchronize()
     log("capturing graphs")
     g_all = capture(torch, lambda: [r.launch(handle) for r in runners], stream)
     g_exp = capture(torch, lambda: [r.launch_experts(handle) for r in runners], stream)
-    g_rtr = capture(torch, lambda: [r.launch_router(handle) for r in runners], stream)
+    g_unf = capture(torch, lambda: [r.launch_unfused(handle) for r in runners], stream)
 
     # warmup then exactly K timed steps (full graph rounds + eager remainder)
     rounds_w = max(1, args.warmup // L)
@@ -193,21 +200,24 @@ def main() -> int:
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for _ in range(full):
-        g_all.replay()
-    with torch.cuda.stream(stream):
+    wall0 = time.perf_counter()
+    with torch.cuda.stream(stream):  # replays and events on the same stream
+        start.record(stream)
+        for _ in range(full):
+            g_all.replay()
         for r in runners[:rem]:
             r.launch(handle)
-    end.record(stream)
+        end.record(stream)
     torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - wall0) * 1e3
     total_ms = start.elapsed_time(end)
+    log(f"timed {args.steps} steps: events {total_ms:.3f} ms, wall {wall_ms:.3f} ms")
     ms_per_step = total_ms / args.steps
     us_per_token = ms_per_step * 1000.0
 
     reps = max(4, args.steps // L)
     exp_ms = time_graph(torch, g_exp, reps, stream) / (reps * L)
-    rtr_ms = time_graph(torch, g_rtr, reps, stream) / (reps * L)
+    unf_ms = time_graph(torch, g_unf, reps, stream) / (reps * L)
     expert_bytes = (TOP_K + 1) * expert_bytes_per_record()
     router_bytes = EXPERTS * HIDDEN * 2
     layer_gbps = expert_bytes / (ms_per_step * 1e-3) / 1e9
@@ -240,8 +250,9 @@ def main() -> int:
                    "router_bytes_per_token": router_bytes},
         "hbm_gbps": round(layer_gbps, 1),
         "hbm_frac": round(layer_gbps / HBM_PEAK_GBPS, 4),
-        "breakdown_us": {"router": round(rtr_ms * 1000, 3), "experts": round(exp_ms * 1000, 3)},
-        "roofline": {"bound": "hbm", "kernel": "mq_moe_decode (expert kernels, 11 experts)",
+        "breakdown_us": {"layer_fused": round(us_per_token, 3), "layer_unfused": round(unf_ms * 1000, 3),
+                         "experts_only": round(exp_ms * 1000, 3)},
+        "roofline": {"bound": "hbm", "kernel": "mq_moe_decode (gate/up + down kernels, 11 experts)",
                      "achieved": round(exp_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(exp_gbps / HBM_PEAK_GBPS, 4), "traffic": None},
         "cpu_baseline": cpu,

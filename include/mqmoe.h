@@ -51,6 +51,12 @@ extern "C" {
  * expert-major record pack `stream_pack` when it is set (same record layout,
  * no header: base = stream_pack + word * pool_stride), else the dense arrays
  * weight [E, out, in/8], scales/biases [E, out, in/group].
+ *
+ * Route words are produced on the device, so kernels bound-check them: a slot
+ * must be < pool_slots, a stream index < stream_records, a dense expert <
+ * the call's expert count.  An out-of-range word is never dereferenced; its
+ * contribution is skipped and a device error flag is raised, reported by
+ * mq_check_device_errors().
  */
 typedef struct MqProjection {
   const uint32_t *weight;
@@ -63,6 +69,8 @@ typedef struct MqProjection {
   uint64_t off_scales;
   uint64_t off_biases;
   const uint8_t *stream_pack;
+  uint32_t pool_slots;      /* records in `pool` */
+  uint32_t stream_records;  /* records in `stream_pack` */
 } MqProjection;
 
 /* Arguments of mq_moe_decode: the fields of the reference's native bridge
@@ -154,11 +162,28 @@ typedef struct MqGroupedArgs {
 /* 1 when a gfx950 device is usable from this process, else 0. */
 int mq_available(void);
 
+/* Allocate the library's per-device workspace (error flags, counters) on the
+ * current device.  Entry points call it lazily, but a first call inside HIP
+ * graph capture cannot allocate: call mq_init() (once per device) before
+ * capturing.  Idempotent. */
+int mq_init(void);
+
 /* Copy the calling thread's last error message into buf (NUL-terminated). */
 int mq_last_error(char *buf, uint32_t max_len);
 
+/* Synchronise `stream`, then read and clear the current device's error flags
+ * raised by kernels (MQ_DEVFLAG_*).  Returns MQ_OK when none were raised,
+ * else MQ_ERR_INVALID with the flags described by mq_last_error(). */
+int mq_check_device_errors(void *stream, uint32_t *flags_out);
+#define MQ_DEVFLAG_BAD_ROUTE 1u /* a route word addressed no valid record/expert */
+
 /* Library version as major*10000 + minor*100 + patch. */
 int mq_version(void);
+
+/* sizeof() of the ABI structs as compiled into the library, so bindings can
+ * verify their layout: which = 0 MqProjection, 1 MqMoeArgs, 2 MqRouteArgs,
+ * 3 MqGroupedArgs; 0 for an unknown id. */
+uint64_t mq_abi_struct_size(int which);
 
 /* ---- record layout (models/flashnext/slab_pack.py:96-149) ---- */
 
@@ -199,6 +224,15 @@ int mq_route_topk(const MqRouteArgs *args, void *stream);
 
 /* ---- decode executor (MetalMoEExecutor.execute, metal_runtime.py:764-932) ---- */
 int mq_moe_decode(const MqMoeArgs *args, void *stream);
+
+/* One routed decode layer, _moe_call with the fused executor
+ * (models/flashnext/adaptive_topk.py:53-292): router logits, then a gate/up
+ * kernel that performs the top-k selection itself (writing route->inds,
+ * scores (bf16), routes, keeps, shared_gate) and runs gate/up/SwiGLU, then
+ * down + combine.  route->x must equal moe->x (bf16); route->logits_out and
+ * route->routes are required; moe->routes/scores/keeps/shared_gate are taken
+ * from the route outputs.  At most 8 tokens; no MQ_DECODE flags. */
+int mq_moe_layer(const MqRouteArgs *route, const MqMoeArgs *moe, void *stream);
 
 /* ---- prefill / verify grouped path ---- */
 uint64_t mq_grouped_workspace_size(uint32_t tokens, uint32_t slots, uint32_t hidden,

@@ -36,7 +36,7 @@ int check_launch(const char *what) {
   return MQ_OK;
 }
 
-int workspace(DeviceWorkspace **out) {
+int workspace(DeviceWorkspace **out, hipStream_t stream) {
   static std::mutex mu;
   static DeviceWorkspace per_device[64];
   static bool ready[64] = {};
@@ -45,6 +45,12 @@ int workspace(DeviceWorkspace **out) {
   if (device < 0 || device >= 64) return fail(MQ_ERR_DEVICE, "device ordinal %d out of range", device);
   std::lock_guard<std::mutex> lock(mu);
   if (!ready[device]) {
+    // Allocating would invalidate a graph being captured on `stream`.
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (stream != nullptr && hipStreamIsCapturing(stream, &status) == hipSuccess &&
+        status != hipStreamCaptureStatusNone)
+      return fail(MQ_ERR_INVALID, "libmqmoe is not initialised on device %d: call mq_init() before graph capture",
+                  device);
     DeviceWorkspace ws{};
     MQ_TRY_HIP(hipMalloc(&ws.counters, kCounterSlots * sizeof(unsigned int)));
     MQ_TRY_HIP(hipMalloc(&ws.flags, kCounterSlots * sizeof(unsigned int)));
@@ -70,6 +76,36 @@ extern "C" int mq_last_error(char *buf, uint32_t max_len) {
 }
 
 extern "C" int mq_version(void) { return 100; }
+
+extern "C" int mq_init(void) {
+  DeviceWorkspace *ws = nullptr;
+  return workspace(&ws, nullptr);
+}
+
+extern "C" int mq_check_device_errors(void *stream, uint32_t *flags_out) {
+  DeviceWorkspace *ws = nullptr;
+  int rc = workspace(&ws, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  MQ_TRY_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  unsigned int flags = 0;
+  MQ_TRY_HIP(hipMemcpy(&flags, ws->flags, sizeof(flags), hipMemcpyDeviceToHost));
+  if (flags) MQ_TRY_HIP(hipMemset(ws->flags, 0, sizeof(unsigned int)));
+  if (flags_out) *flags_out = flags;
+  if (flags & MQ_DEVFLAG_BAD_ROUTE)
+    return fail(MQ_ERR_INVALID, "a kernel skipped a route word that addressed no valid record or expert");
+  if (flags) return fail(MQ_ERR_INVALID, "device error flags 0x%x", flags);
+  return MQ_OK;
+}
+
+extern "C" uint64_t mq_abi_struct_size(int which) {
+  switch (which) {
+    case 0: return sizeof(MqProjection);
+    case 1: return sizeof(MqMoeArgs);
+    case 2: return sizeof(MqRouteArgs);
+    case 3: return sizeof(MqGroupedArgs);
+    default: return 0;
+  }
+}
 
 extern "C" int mq_available(void) {
   int count = 0;

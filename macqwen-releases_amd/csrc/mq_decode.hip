@@ -1,15 +1,17 @@
-// Decode-path kernels for gfx950: Q4 QMV, fused gate/up + SwiGLU, and
-// down + score combine + shared epilogue.
+// Decode-path kernels for gfx950: Q4 QMV, fused gate/up + SwiGLU (with the
+// router selection folded in), and down + score combine + shared epilogue.
 //
-// Work mapping.  A wave64 is four 16-lane slices (one DPP row each).  A slice
-// computes one output row: lane i of the slice owns the CPL consecutive
-// 32-input chunks [i*CPL, (i+1)*CPL) of the row, loads them with 128-bit
-// loads (one chunk = 4 uint32 = 32 nibbles), dequantises in registers into
-// bf16 pairs (128+q) and accumulates with v_dot2_f32_bf16 against the
-// activation chunk it keeps in registers.  The row sum is a 4-step DPP
-// reduction inside the slice, so a wave retires four rows per step with no
-// LDS traffic.  Input widths that are multiples of 512 (16 lanes x 32) use
-// every lane; other multiples of 32 mask the tail chunks.
+// Row engine.  A row of a Q4 matrix is cut into 32-input chunks (one chunk =
+// 4 uint32 = 32 nibbles = one 128-bit load).  A "slice" of SW lanes (SW = 64
+// or 16) owns one output row per step: lane li loads chunks {li, li+SW, ...}
+// (CPL chunks), so each load instruction of a slice reads SW*16 contiguous
+// bytes.  Weights are streamed with non-temporal loads.  Nibble pairs are
+// turned into bf16 pairs (128+q) with one v_bfi_b32 each and multiplied with
+// the activation chunk (kept in registers as matching bf16 pairs) by
+// v_dot2_f32_bf16; the 128 offset is removed with the chunk sum, and the group
+// scale/bias are applied in float32.  A slice reduces its row with DPP
+// (16 lanes) or DPP + readlane (64 lanes).  Every wave issues all of its loads
+// before its first dependent instruction.
 //
 // Rounding points follow the reference executor
 // (models/flashnext/metal_runtime.py:231-336): every projection output is
@@ -19,18 +21,81 @@
 #include <math.h>
 
 #include "mq_internal.h"
+#include "mq_select.h"
 
 namespace mq {
+
+int launch_router_logits(const uint16_t *x, const uint16_t *gate_w, const uint16_t *shared_gate_w,
+                         uint16_t *logits, uint16_t *shared_logit, uint32_t tokens, uint32_t hidden,
+                         uint32_t routed_rows, hipStream_t stream);
+int validate_route_args(const MqRouteArgs &a);
+SelectParams select_params(const MqRouteArgs &a, const uint16_t *logits);
+
 namespace {
 
-constexpr int kWaves = 4;           // waves per block
+constexpr int kWaves = 4;  // waves per block
 constexpr int kThreads = 64 * kWaves;
-constexpr int kRowsPerWave = 4;     // one row per 16-lane slice
+constexpr uint32_t kMaxSlots = 16;      // routed slots per token in the fused kernels
+constexpr uint32_t kMaxLayerTokens = 8;  // tokens of the fused routed layer
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------------ slices
+template <int SW>
+struct Slice {
+  static_assert(SW == 16 || SW == 64, "slice width must be 16 or 64 lanes");
+  static constexpr int kRows = 64 / SW;  // rows per wave step
+  __device__ static __forceinline__ int sub(int lane) { return lane / SW; }
+  __device__ static __forceinline__ int li(int lane) { return lane % SW; }
+  // Row sum; valid in lane 0 of the slice (all lanes for SW = 64).
+  __device__ static __forceinline__ float reduce(float v) {
+    if constexpr (SW == 16) return row16_sum(v);
+    else return wave_sum(v);
+  }
+};
+
+__device__ __forceinline__ uint4 ld_nt(const uint32_t *p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// (128+q_k, 128+q_{k+4}) bf16 pair from nibbles k and k+4 of w (one v_bfi_b32).
+__device__ __forceinline__ uint32_t nib_pair_bfi(uint32_t w, int k) {
+  uint32_t r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(0x000f000fu), "v"(w >> (4 * k)), "v"(0x43004300u));
+  return r;
+}
+
+// Four independent accumulation chains (one per packed word) for ILP.
+__device__ __forceinline__ float q4_dot(const uint4 &w, const XChunk &x) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  float d[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    d[j] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) d[j] = dot2_bf16(x.p[4 * j + k], nib_pair_bfi(ws[j], k), d[j]);
+  }
+  return ((d[0] + d[1]) + (d[2] + d[3])) - 128.0f * x.osum;
+}
+
+// Sum of the 32 bf16 values of a chunk (four independent chains).
+__device__ __forceinline__ float pair_sum4(const XChunk &x) {
+  float s[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    s[j] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s[j] = dot2_bf16(x.p[4 * j + k], 0x3f803f80u, s[j]);
+  }
+  return (s[0] + s[1]) + (s[2] + s[3]);
+}
 
 // ------------------------------------------------------------------ activations
-
 // Activation chunk(s) of one lane: bf16 inputs need one pair chunk, float32
-// inputs are split into bf16 hi + lo chunks (x = hi + lo to 16 bits).
+// inputs are split into bf16 hi + lo chunks (x = hi + lo to 16 bits).  The
+// loads are issued by issue() and consumed by finish(), so a kernel can put
+// the (cache-resident) activation loads ahead of its weight stream and convert
+// them while the weights are still in flight.
 template <class TT>
 struct XLane;
 
@@ -39,26 +104,19 @@ struct XLane<BF16T> {
   static constexpr int kParts = 1;
   XChunk part[1];
   float bias_sum;  // sum of the inputs, multiplies the group bias
-  __device__ __forceinline__ void load(const uint16_t *src, bool valid) {
-    if (valid) {
-      const uint4 *v = reinterpret_cast<const uint4 *>(src);
+  uint4 raw[4];
+  __device__ __forceinline__ void issue(const uint16_t *src, bool valid) {
+    const uint4 *v = reinterpret_cast<const uint4 *>(src);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint4 q = v[j];
-        const uint32_t u[4] = {q.x, q.y, q.z, q.w};
-        pairs_from_words(u, &part[0].p[4 * j]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) part[0].p[i] = 0u;
-    }
-    part[0].osum = chunk_pair_sum(part[0]);
-    bias_sum = part[0].osum;
+    for (int j = 0; j < 4; ++j) raw[j] = valid ? v[j] : make_uint4(0u, 0u, 0u, 0u);
   }
-  __device__ __forceinline__ void load_words(const uint32_t w[16]) {
+  __device__ __forceinline__ void finish() {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) pairs_from_words(&w[4 * j], &part[0].p[4 * j]);
-    part[0].osum = chunk_pair_sum(part[0]);
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t u[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+      pairs_from_words(u, &part[0].p[4 * j]);
+    }
+    part[0].osum = pair_sum4(part[0]);
     bias_sum = part[0].osum;
   }
 };
@@ -68,47 +126,61 @@ struct XLane<F32T> {
   static constexpr int kParts = 2;
   XChunk part[2];
   float bias_sum;
-  __device__ __forceinline__ void load(const float *src, bool valid) {
+  float4 raw[8];
+  __device__ __forceinline__ void issue(const float *src, bool valid) {
+    const float4 *v = reinterpret_cast<const float4 *>(src);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) raw[j] = valid ? v[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  __device__ __forceinline__ void finish() {
     uint32_t hi[16], lo[16];
     float s = 0.0f;
-    if (valid) {
-      const float4 *v = reinterpret_cast<const float4 *>(src);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float4 q = v[j];
-        const float f[4] = {q.x, q.y, q.z, q.w};
+    for (int j = 0; j < 8; ++j) {
+      const float f[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int idx = 4 * j + k;
-          const uint16_t h = f32_to_bf16(f[k]);
-          const uint16_t l = f32_to_bf16(f[k] - bf16_to_f32(h));
-          s += f[k];
-          if (idx & 1) {
-            hi[idx >> 1] |= static_cast<uint32_t>(h) << 16;
-            lo[idx >> 1] |= static_cast<uint32_t>(l) << 16;
-          } else {
-            hi[idx >> 1] = h;
-            lo[idx >> 1] = l;
-          }
+      for (int k = 0; k < 4; ++k) {
+        const int idx = 4 * j + k;
+        const uint16_t h = f32_to_bf16(f[k]);
+        const uint16_t l = f32_to_bf16(f[k] - bf16_to_f32(h));
+        s += f[k];
+        if (idx & 1) {
+          hi[idx >> 1] |= static_cast<uint32_t>(h) << 16;
+          lo[idx >> 1] |= static_cast<uint32_t>(l) << 16;
+        } else {
+          hi[idx >> 1] = h;
+          lo[idx >> 1] = l;
         }
       }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) hi[i] = lo[i] = 0u;
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       pairs_from_words(&hi[4 * j], &part[0].p[4 * j]);
       pairs_from_words(&lo[4 * j], &part[1].p[4 * j]);
     }
-    part[0].osum = chunk_pair_sum(part[0]);
-    part[1].osum = chunk_pair_sum(part[1]);
+    part[0].osum = pair_sum4(part[0]);
+    part[1].osum = pair_sum4(part[1]);
     bias_sum = s;
   }
 };
 
-// ------------------------------------------------------------------ weight rows
+template <class TT, int SW, int CPL>
+__device__ __forceinline__ void issue_x(XLane<TT> *x, const typename TT::storage *src, uint32_t in_w, int li) {
+  const uint32_t chunks = in_w >> 5;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const uint32_t c = static_cast<uint32_t>(j * SW + li);
+    x[j].issue(src + c * 32, c < chunks);
+  }
+}
 
+template <class TT, int CPL>
+__device__ __forceinline__ void finish_x(XLane<TT> *x) {
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) x[j].finish();
+}
+
+// ------------------------------------------------------------------ weight rows
 template <int CPL>
 struct RowLoad {
   uint4 w[CPL];
@@ -117,18 +189,18 @@ struct RowLoad {
 };
 
 // Issue the loads of one lane's chunks of row `row` (masked chunks read as 0).
-template <int CPL>
-__device__ __forceinline__ void load_row(RowLoad<CPL> &r, const ExpertPtrs &e, uint32_t row,
-                                         uint32_t in_w, uint32_t group, int li, bool row_ok) {
+template <int SW, int CPL>
+__device__ __forceinline__ void load_row(RowLoad<CPL> &r, const ExpertPtrs &e, uint32_t row, uint32_t in_w,
+                                         uint32_t group, int li, bool row_ok) {
   const uint32_t chunks = in_w >> 5;
   const uint32_t words = in_w >> 3;
   const uint32_t groups = in_w / group;
   const uint32_t shift = group == 64 ? 1 : 0;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const uint32_t c = static_cast<uint32_t>(li) * CPL + j;
+    const uint32_t c = static_cast<uint32_t>(j * SW + li);
     if (row_ok && c < chunks) {
-      r.w[j] = *reinterpret_cast<const uint4 *>(e.w + static_cast<uint64_t>(row) * words + c * 4);
+      r.w[j] = ld_nt(e.w + static_cast<uint64_t>(row) * words + c * 4);
       const uint64_t gi = static_cast<uint64_t>(row) * groups + (c >> shift);
       r.s[j] = e.s[gi];
       r.b[j] = e.b[gi];
@@ -148,26 +220,14 @@ __device__ __forceinline__ float row_partial(const RowLoad<CPL> &r, const XLane<
   for (int j = 0; j < CPL; ++j) {
     float dq = 0.0f;
 #pragma unroll
-    for (int p = 0; p < XLane<TT>::kParts; ++p) dq += q4_chunk_dot(r.w[j], x[j].part[p]);
+    for (int p = 0; p < XLane<TT>::kParts; ++p) dq += q4_dot(r.w[j], x[j].part[p]);
     acc = fmaf(bf16_to_f32(r.s[j]), dq, acc);
     acc = fmaf(bf16_to_f32(r.b[j]), x[j].bias_sum, acc);
   }
   return acc;
 }
 
-template <class TT, int CPL>
-__device__ __forceinline__ void load_x(XLane<TT> *x, const typename TT::storage *src, uint32_t in_w,
-                                       int li) {
-  const uint32_t chunks = in_w >> 5;
-#pragma unroll
-  for (int j = 0; j < CPL; ++j) {
-    const uint32_t c = static_cast<uint32_t>(li) * CPL + j;
-    x[j].load(src + c * 32, c < chunks);
-  }
-}
-
 // ------------------------------------------------------------------ SwiGLU
-
 // MLX's sigmoid sequence with each step rounded to T
 // (models/flashnext/metal_runtime.py:278-284): m=|g|; e=T(exp(m));
 // d=T(1+e); s=T(1/d); sig = g<0 ? s : T(1-s).  exp is the float32
@@ -175,7 +235,11 @@ __device__ __forceinline__ void load_x(XLane<TT> *x, const typename TT::storage 
 template <class TT>
 __device__ __forceinline__ float sigmoid_t(float g) {
   const float m = fabsf(g);
-  const float e = TT::round(static_cast<float>(exp(static_cast<double>(m))));
+  float e;
+  if constexpr (TT::dtype == MQ_BF16)
+    e = exp_bf16(m);  // guarded float32 exp, float64 only near a bf16 midpoint
+  else
+    e = static_cast<float>(exp(static_cast<double>(m)));
   const float d = TT::round(__fadd_rn(1.0f, e));
   const float s = TT::round(__fdiv_rn(1.0f, d));
   const float om = TT::round(__fsub_rn(1.0f, s));
@@ -197,96 +261,188 @@ struct SharedExpert {
   MqProjection p[3];  // gate, up, down; addressed with route word 0
 };
 
-// Projection QMV: out[pair, row] = T(W_route(pair) . x(pair)).
-// Grid: one wave per 4-row tile; tiles enumerate (pair, row/4).
-template <class TT, int CPL>
+// Projection QMV: out[pair, row] = T(W_route(pair) . x(pair)).  A wave handles
+// R steps of Slice<SW>::kRows rows of one pair.
+template <class TT, int SW, int CPL, int R>
 __global__ __launch_bounds__(kThreads) void gather_qmv_kernel(
     const typename TT::storage *__restrict__ x, int slot_input, MqProjection proj,
-    const uint32_t *__restrict__ routes, typename TT::storage *__restrict__ out,
-    uint32_t pairs, uint32_t slots, uint32_t in_w, uint32_t out_w, uint32_t group) {
+    const uint32_t *__restrict__ routes, typename TT::storage *__restrict__ out, uint32_t pairs, uint32_t slots,
+    uint32_t in_w, uint32_t out_w, uint32_t group, uint32_t dense_count, unsigned int *__restrict__ err) {
   using S = typename TT::storage;
+  using Sl = Slice<SW>;
+  constexpr int kTileRows = R * Sl::kRows;
   const int lane = threadIdx.x & 63;
-  const int li = lane & 15;
-  const int slice = lane >> 4;
-  const uint32_t tiles_per_pair = (out_w + kRowsPerWave - 1) / kRowsPerWave;
+  const int li = Sl::li(lane);
+  const int sub = Sl::sub(lane);
+  const uint32_t tiles_per_pair = (out_w + kTileRows - 1) / kTileRows;
   const uint32_t tile = blockIdx.x * kWaves + (threadIdx.x >> 6);
   if (tile >= pairs * tiles_per_pair) return;  // wave-uniform
   const uint32_t pair = tile / tiles_per_pair;
-  const uint32_t row = (tile % tiles_per_pair) * kRowsPerWave + slice;
-  const bool row_ok = row < out_w;
+  const uint32_t row0 = (tile % tiles_per_pair) * kTileRows;
   const uint32_t word = routes ? routes[pair] : 0u;
-  const ExpertPtrs e = expert_ptrs(proj, word, out_w, in_w, group);
-
-  RowLoad<CPL> r;
-  load_row<CPL>(r, e, row, in_w, group, li, row_ok);
+  const ExpertPtrs e = expert_ptrs(proj, word, out_w, in_w, group, dense_count);
+  if (!e.ok) {  // wave-uniform: the word belongs to the wave's pair
+    if (lane == 0) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
+    return;
+  }
   const uint32_t token = pair / slots;
   const S *src = x + static_cast<uint64_t>(slot_input ? pair : token) * in_w;
   XLane<TT> xl[CPL];
-  load_x<TT, CPL>(xl, src, in_w, li);
-  const float v = row16_sum(row_partial<TT, CPL>(r, xl));
-  if (li == 0 && row_ok) out[static_cast<uint64_t>(pair) * out_w + row] = TT::store(v);
+  issue_x<TT, SW, CPL>(xl, src, in_w, li);
+  RowLoad<CPL> r[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const uint32_t row = row0 + i * Sl::kRows + sub;
+    load_row<SW, CPL>(r[i], e, row, in_w, group, li, row < out_w);
+  }
+  finish_x<TT, CPL>(xl);
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const uint32_t row = row0 + i * Sl::kRows + sub;
+    const float v = Sl::reduce(row_partial<TT, CPL>(r[i], xl));
+    if (li == 0 && row < out_w) out[static_cast<uint64_t>(pair) * out_w + row] = TT::store(v);
+  }
 }
 
-// Fused gate + up + SwiGLU: act[pair, row] = swiglu(T(gate), T(up)).
-// Pairs [0, tokens*slots) are routed; with a shared expert, pairs
-// [tokens*slots, tokens*slots + tokens) are the shared expert of each token.
-template <class TT, int CPL>
-__global__ __launch_bounds__(kThreads) void gateup_swiglu_kernel(
-    const typename TT::storage *__restrict__ x, MqProjection gate, MqProjection up,
-    SharedExpert shared, const uint32_t *__restrict__ routes,
-    const int32_t *__restrict__ keeps, typename TT::storage *__restrict__ act,
-    typename TT::storage *__restrict__ gate_out, typename TT::storage *__restrict__ up_out,
-    uint32_t tokens, uint32_t slots, uint32_t pair_base, uint32_t pairs, uint32_t hidden,
-    uint32_t inter, uint32_t group) {
-  using S = typename TT::storage;
-  const int lane = threadIdx.x & 63;
-  const int li = lane & 15;
-  const int slice = lane >> 4;
-  const uint32_t tiles_per_pair = (inter + kRowsPerWave - 1) / kRowsPerWave;
-  const uint32_t tile = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  if (tile >= pairs * tiles_per_pair) return;
-  const uint32_t pair = pair_base + tile / tiles_per_pair;
-  const uint32_t row = (tile % tiles_per_pair) * kRowsPerWave + slice;
-  const bool row_ok = row < inter;
-  const uint32_t routed_pairs = tokens * slots;
-  const bool is_shared = pair >= routed_pairs;
-  const uint32_t token = is_shared ? pair - routed_pairs : pair / slots;
-  if (!is_shared && keeps != nullptr && (pair % slots) >= static_cast<uint32_t>(keeps[token])) return;
+// Router selection staged in LDS for the fused layer kernel.
+struct RouteLds {
+  uint32_t word[kMaxLayerTokens * kMaxSlots];
+  int32_t keep[kMaxLayerTokens];
+};
 
-  MqProjection gp, upp;
-  uint32_t word;
-  if (is_shared) {
-    gp = shared.p[0];
-    upp = shared.p[1];
-    word = 0u;
-  } else {
-    gp = gate;
-    upp = up;
-    word = routes[pair];
+struct SelectOutputs {  // global outputs of the selection (written by block 0)
+  uint32_t *inds;
+  uint16_t *scores;     // bf16
+  uint16_t *scores_raw;
+  uint32_t *routes;
+  int32_t *keeps;
+  uint16_t *shared_gate;
+  const uint16_t *shared_logit;
+};
+
+// Fused gate + up + SwiGLU: act[pair, row] = swiglu(T(gate), T(up)).
+// Pairs [0, tokens*slots) are routed, pairs [tokens*slots, +tokens) are the
+// shared expert of each token.  Tiles run the shared pairs first (they do not
+// depend on routing).  With SELECT, every block that has routed tiles runs
+// the router selection itself (one wave per token, from the logits) and keeps
+// the route words in LDS; block 0 also publishes the selection.
+template <class TT, int SW, int CPL, int R, bool SELECT>
+__global__ __launch_bounds__(kThreads) void gateup_kernel(
+    const typename TT::storage *__restrict__ x, MqProjection gate, MqProjection up, SharedExpert shared,
+    bool has_shared, const uint32_t *__restrict__ routes, const int32_t *__restrict__ keeps, SelectParams sel,
+    SelectOutputs sel_out, typename TT::storage *__restrict__ act, typename TT::storage *__restrict__ gate_out,
+    typename TT::storage *__restrict__ up_out, uint32_t tokens, uint32_t slots, uint32_t hidden, uint32_t inter,
+    uint32_t group, uint32_t dense_count, uint32_t tile_limit, unsigned int *__restrict__ err) {
+  using Sl = Slice<SW>;
+  constexpr int kTileRows = R * Sl::kRows;
+  __shared__ RouteLds lds;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int li = Sl::li(lane);
+  const int sub = Sl::sub(lane);
+  const uint32_t tiles_per_pair = (inter + kTileRows - 1) / kTileRows;
+  const uint32_t routed_pairs = tokens * slots;
+  const uint32_t shared_pairs = has_shared ? tokens : 0u;
+  const uint32_t total_tiles = min((routed_pairs + shared_pairs) * tiles_per_pair, tile_limit);
+  const uint32_t shared_tiles = shared_pairs * tiles_per_pair;
+  const uint32_t block_first = blockIdx.x * kWaves;
+
+  if constexpr (SELECT) {
+    // Does this block own any routed tile?  (uniform per block)
+    const uint32_t block_last = min(block_first + kWaves, total_tiles);
+    if (block_last > shared_tiles || blockIdx.x == 0) {
+      for (uint32_t t = wave; t < tokens; t += kWaves) {
+        const SelectLane s = select_token(sel, t, lane);
+        if (static_cast<uint32_t>(lane) < slots) lds.word[t * slots + lane] = s.word;
+        if (lane == 0) lds.keep[t] = static_cast<int32_t>(s.keep);
+        if (blockIdx.x == 0) {
+          const uint64_t base = static_cast<uint64_t>(t) * slots;
+          if (static_cast<uint32_t>(lane) < slots) {
+            sel_out.inds[base + lane] = s.ind;
+            sel_out.scores[base + lane] = f32_to_bf16(s.score);
+            if (sel_out.scores_raw) sel_out.scores_raw[base + lane] = f32_to_bf16(s.raw);
+            sel_out.routes[base + lane] = s.word;
+          } else if (lane == 63) {
+            if (sel_out.keeps) sel_out.keeps[t] = static_cast<int32_t>(s.keep);
+            if (sel_out.shared_gate)
+              sel_out.shared_gate[t] = f32_to_bf16(sigmoid_bf16(bf16_to_f32(sel_out.shared_logit[t])));
+          }
+        }
+      }
+      __syncthreads();
+    }
   }
-  const ExpertPtrs eg = expert_ptrs(gp, word, inter, hidden, group);
-  const ExpertPtrs eu = expert_ptrs(upp, word, inter, hidden, group);
-  RowLoad<CPL> rg, ru;
-  load_row<CPL>(rg, eg, row, hidden, group, li, row_ok);
-  load_row<CPL>(ru, eu, row, hidden, group, li, row_ok);
+
+  const uint32_t tile = block_first + wave;
+  if (tile >= total_tiles) return;
+  // Shared tiles first, then routed tiles.
+  const bool is_shared = tile < shared_tiles;
+  const uint32_t local = is_shared ? tile : tile - shared_tiles;
+  const uint32_t pair = is_shared ? routed_pairs + local / tiles_per_pair : local / tiles_per_pair;
+  const uint32_t row0 = (local % tiles_per_pair) * kTileRows;
+  const uint32_t token = is_shared ? pair - routed_pairs : pair / slots;
+  uint32_t word = 0u;
+  if (!is_shared) {
+    int32_t keep_t;
+    if constexpr (SELECT) {
+      word = lds.word[pair];
+      keep_t = lds.keep[token];
+    } else {
+      word = routes[pair];
+      keep_t = keeps != nullptr ? keeps[token] : static_cast<int32_t>(slots);
+    }
+    if ((pair % slots) >= static_cast<uint32_t>(keep_t)) return;  // padded slot
+  }
+  // Wave-uniform branch (choosing a projection by reference would copy the
+  // kernel-argument structs to private memory).
+  ExpertPtrs eg, eu;
+  if (is_shared) {
+    eg = expert_ptrs(shared.p[0], 0u, inter, hidden, group, 1u);
+    eu = expert_ptrs(shared.p[1], 0u, inter, hidden, group, 1u);
+  } else {
+    eg = expert_ptrs(gate, word, inter, hidden, group, dense_count);
+    eu = expert_ptrs(up, word, inter, hidden, group, dense_count);
+  }
+  if (!eg.ok || !eu.ok) {
+    if (lane == 0) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
+    return;
+  }
   XLane<TT> xl[CPL];
-  load_x<TT, CPL>(xl, x + static_cast<uint64_t>(token) * hidden, hidden, li);
-  const float g = row16_sum(row_partial<TT, CPL>(rg, xl));
-  const float u = row16_sum(row_partial<TT, CPL>(ru, xl));
-  if (li == 0 && row_ok) {
-    const float gt = TT::round(g);
-    const float ut = TT::round(u);
-    const uint64_t idx = static_cast<uint64_t>(pair) * inter + row;
-    act[idx] = TT::store(swiglu_t<TT>(gt, ut));
-    if (gate_out != nullptr && !is_shared) gate_out[idx] = TT::store(gt);
-    if (up_out != nullptr && !is_shared) up_out[idx] = TT::store(ut);
+  issue_x<TT, SW, CPL>(xl, x + static_cast<uint64_t>(token) * hidden, hidden, li);
+  RowLoad<CPL> rg[R], ru[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const uint32_t row = row0 + i * Sl::kRows + sub;
+    load_row<SW, CPL>(rg[i], eg, row, hidden, group, li, row < inter);
+    load_row<SW, CPL>(ru[i], eu, row, hidden, group, li, row < inter);
+  }
+  finish_x<TT, CPL>(xl);
+  float gv[R], uv[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    gv[i] = Sl::reduce(row_partial<TT, CPL>(rg[i], xl));
+    uv[i] = Sl::reduce(row_partial<TT, CPL>(ru[i], xl));
+  }
+  // Epilogue: one lane per row (lane i of the wave for SW = 64, lane 0 of each
+  // slice for SW = 16), so the double-precision exp runs in parallel.
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const bool mine = SW == 64 ? (lane == i) : (li == 0);
+    const uint32_t row = row0 + i * Sl::kRows + sub;
+    if (mine && row < inter) {
+      const float gt = TT::round(gv[i]);
+      const float ut = TT::round(uv[i]);
+      const uint64_t idx = static_cast<uint64_t>(pair) * inter + row;
+      act[idx] = TT::store(swiglu_t<TT>(gt, ut));
+      if (gate_out != nullptr && !is_shared) gate_out[idx] = TT::store(gt);
+      if (up_out != nullptr && !is_shared) up_out[idx] = TT::store(ut);
+    }
   }
 }
 
 // SwiGLU over precomputed T gate/up projections (unfused path).
 template <class TT>
-__global__ void swiglu_kernel(const typename TT::storage *__restrict__ g,
-                              const typename TT::storage *__restrict__ u,
+__global__ void swiglu_kernel(const typename TT::storage *__restrict__ g, const typename TT::storage *__restrict__ u,
                               typename TT::storage *__restrict__ out, uint64_t n) {
   const uint64_t i = static_cast<uint64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) out[i] = TT::store(swiglu_t<TT>(TT::load(g[i]), TT::load(u[i])));
@@ -294,78 +450,171 @@ __global__ void swiglu_kernel(const typename TT::storage *__restrict__ g,
 
 enum SharedMode : int { kSharedNone = 0, kSharedY = 1, kSharedParts = 2, kSharedExpert = 3 };
 
-// Down + score combine + shared epilogue for one token and four output rows
-// per wave.  For each routed slot s < keep: d = T(W_down . act[t,s]);
-// acc += float(d) * float(score[t,s]) in float32 with no contraction
-// (models/flashnext/metal_runtime.py:291-336).  The activations of the
-// block's token are staged in LDS once per block.
-template <class TT, int CPL>
+// Activation staging in LDS for the down kernel.  Each 32-input chunk of each
+// source row (routed slot or shared expert) is stored already converted to the
+// pair layout, plane-major so that consecutive lanes read consecutive 16-byte
+// words: plane q (q < 4*kParts) holds word q of every chunk, followed by
+// kParts chunk sums and the bias sum.
+template <class TT>
+struct StagedX {
+  static constexpr int kParts = XLane<TT>::kParts;
+  static constexpr uint32_t kBytesPerChunk = kParts * 64 + (kParts + 1) * 4;
+  uint4 *q;
+  float *sums;
+  uint32_t units;
+  __device__ __forceinline__ StagedX(unsigned char *smem, uint32_t n_units)
+      : q(reinterpret_cast<uint4 *>(smem)),
+        sums(reinterpret_cast<float *>(smem + static_cast<size_t>(n_units) * kParts * 64)),
+        units(n_units) {}
+  __device__ __forceinline__ void store(const XLane<TT> &x, uint32_t u) const {
+#pragma unroll
+    for (int p = 0; p < kParts; ++p) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        q[(p * 4 + w) * units + u] = make_uint4(x.part[p].p[4 * w], x.part[p].p[4 * w + 1], x.part[p].p[4 * w + 2],
+                                                x.part[p].p[4 * w + 3]);
+      sums[p * units + u] = x.part[p].osum;
+    }
+    sums[kParts * units + u] = x.bias_sum;
+  }
+  __device__ __forceinline__ void load(XLane<TT> &x, uint32_t u) const {
+#pragma unroll
+    for (int p = 0; p < kParts; ++p) {
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint4 v = q[(p * 4 + w) * units + u];
+        x.part[p].p[4 * w] = v.x;
+        x.part[p].p[4 * w + 1] = v.y;
+        x.part[p].p[4 * w + 2] = v.z;
+        x.part[p].p[4 * w + 3] = v.w;
+      }
+      x.part[p].osum = sums[p * units + u];
+    }
+    x.bias_sum = sums[kParts * units + u];
+  }
+};
+
+// Down + score combine + shared epilogue for one token and Slice<SW>::kRows
+// output rows per wave.  For each routed slot s < keep: d = T(W_down .
+// act[t,s]); acc += float(d) * float(score[t,s]) in float32 with no
+// contraction, in slot order (models/flashnext/metal_runtime.py:291-336).
+//
+// Order of work: route words, scores and the first activation chunk of each
+// thread are loaded first; then every slot's weight rows are issued (NS slots
+// including the shared expert, inactive ones masked to zero); the activation
+// chunks are converted into LDS while the weights are in flight; finally all
+// NS row dots are computed without branches (independent chains) and
+// combined in slot order.
+template <class TT, int SW, int CPL, int NS>
 __global__ __launch_bounds__(kThreads) void down_combine_kernel(
-    const typename TT::storage *__restrict__ act, MqProjection down,
-    SharedExpert shared, const uint32_t *__restrict__ routes,
-    const void *__restrict__ scores, int score_dtype, const int32_t *__restrict__ keeps,
-    int shared_mode, const typename TT::storage *__restrict__ shared_vec,
-    const uint16_t *__restrict__ shared_gate, typename TT::storage *__restrict__ out,
-    uint32_t tokens, uint32_t slots, uint32_t hidden, uint32_t inter, uint32_t group,
-    uint32_t tiles_per_token) {
+    const typename TT::storage *__restrict__ act, MqProjection down, SharedExpert shared,
+    const uint32_t *__restrict__ routes, const void *__restrict__ scores, int score_dtype,
+    const int32_t *__restrict__ keeps, int shared_mode, const typename TT::storage *__restrict__ shared_vec,
+    const uint16_t *__restrict__ shared_gate, typename TT::storage *__restrict__ out, uint32_t tokens,
+    uint32_t slots, uint32_t hidden, uint32_t inter, uint32_t group, uint32_t tiles_per_token,
+    uint32_t dense_count, unsigned int *__restrict__ err) {
   using S = typename TT::storage;
+  using Sl = Slice<SW>;
   extern __shared__ __align__(16) unsigned char smem[];
-  S *lds_act = reinterpret_cast<S *>(smem);
 
   const int lane = threadIdx.x & 63;
-  const int li = lane & 15;
-  const int slice = lane >> 4;
+  const int li = Sl::li(lane);
+  const int sub = Sl::sub(lane);
   const uint32_t token = blockIdx.y;
   const uint32_t tile = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  const uint32_t row = tile * kRowsPerWave + slice;
-  const bool row_ok = tile < tiles_per_token && row < hidden;
-  const uint32_t keep = keeps ? static_cast<uint32_t>(keeps[token]) : slots;
+  const bool tile_ok = tile < tiles_per_token;
+  const uint32_t row = tile * Sl::kRows + sub;
+  const bool row_ok = tile_ok && row < hidden;
+  const uint32_t keep = keeps ? min(static_cast<uint32_t>(keeps[token]), slots) : slots;
   const bool with_shared_expert = shared_mode == kSharedExpert;
   const uint32_t n_src = slots + (with_shared_expert ? 1u : 0u);
+  const uint32_t cps = inter >> 5;  // chunks per source row
+  const uint32_t units = n_src * cps;
+  const StagedX<TT> stage(smem, units);
 
-  // Stage this token's activations: routed pairs, then the shared pair.
+  // Small per-token inputs first.
+  uint32_t word[NS];
+  float score[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    word[s] = 0u;
+    score[s] = 0.0f;
+    if (static_cast<uint32_t>(s) < keep) {
+      const uint64_t pair = static_cast<uint64_t>(token) * slots + s;
+      word[s] = routes[pair];
+      score[s] = score_dtype == MQ_BF16 ? bf16_to_f32(static_cast<const uint16_t *>(scores)[pair])
+                                        : static_cast<const float *>(scores)[pair];
+    }
+  }
   const uint32_t routed_pairs = tokens * slots;
-  const uint32_t elems = n_src * inter;
-  const uint32_t vec = 16 / sizeof(S);
-  for (uint32_t i = threadIdx.x * vec; i < elems; i += kThreads * vec) {
-    const uint32_t src_pair_local = i / inter;
-    const uint32_t col = i % inter;
-    const uint64_t pair = src_pair_local < slots
-                              ? static_cast<uint64_t>(token) * slots + src_pair_local
-                              : static_cast<uint64_t>(routed_pairs) + token;
-    if (src_pair_local < slots && src_pair_local >= keep) continue;
-    *reinterpret_cast<uint4 *>(&lds_act[i]) =
-        *reinterpret_cast<const uint4 *>(&act[pair * inter + col]);
+  auto unit_source = [&](uint32_t u, bool &valid) -> const S * {
+    const uint32_t src = u / cps;
+    const uint32_t c = u % cps;
+    valid = u < units && (src >= slots || src < keep);
+    const uint64_t pair = src < slots ? static_cast<uint64_t>(token) * slots + src
+                                      : static_cast<uint64_t>(routed_pairs) + token;
+    return act + pair * inter + c * 32u;
+  };
+  XLane<TT> first;
+  bool first_ok;
+  const S *first_src = unit_source(threadIdx.x, first_ok);
+  first.issue(first_src, first_ok);
+
+  RowLoad<CPL> rows[NS];
+  bool slot_ok[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const uint32_t su = static_cast<uint32_t>(s);
+    const bool routed = su < keep;
+    const bool is_shared = with_shared_expert && su == slots;
+    ExpertPtrs e{nullptr, nullptr, nullptr, false};
+    if (routed) e = expert_ptrs(down, word[s], hidden, inter, group, dense_count);
+    else if (is_shared) e = expert_ptrs(shared.p[2], 0u, hidden, inter, group, 1u);
+    slot_ok[s] = e.ok;
+    if ((routed || is_shared) && !e.ok && lane == 0 && tile_ok) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
+    load_row<SW, CPL>(rows[s], e, row, inter, group, li, row_ok && e.ok);
+  }
+
+  first.finish();
+  if (first_ok) stage.store(first, threadIdx.x);
+  for (uint32_t u = threadIdx.x + kThreads; u < units; u += kThreads) {
+    bool ok;
+    const S *src = unit_source(u, ok);
+    if (ok) {
+      XLane<TT> x;
+      x.issue(src, true);
+      x.finish();
+      stage.store(x, u);
+    }
   }
   __syncthreads();
-  if (!(tile < tiles_per_token)) return;
+  if (!tile_ok) return;
 
-  float acc = 0.0f;
-  for (uint32_t s = 0; s < slots; ++s) {
-    if (s >= keep) break;  // padded slots carry score 0 and add exact zeros
-    const uint32_t pair = token * slots + s;
-    const ExpertPtrs e = expert_ptrs(down, routes[pair], hidden, inter, group);
-    RowLoad<CPL> r;
-    load_row<CPL>(r, e, row, inter, group, li, row_ok);
+  float v[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    // Inactive slots have all-zero weight rows and read slot 0's activations,
+    // so they add nothing; computing them keeps the loop free of branches.
+    const uint32_t su = static_cast<uint32_t>(s);
+    const bool active = su < keep || (with_shared_expert && su == slots);
+    const uint32_t src = active ? su : 0u;
     XLane<TT> xl[CPL];
-    load_x<TT, CPL>(xl, lds_act + s * inter, inter, li);
-    const float v = row16_sum(row_partial<TT, CPL>(r, xl));
-    const float score = score_dtype == MQ_BF16
-                            ? bf16_to_f32(static_cast<const uint16_t *>(scores)[pair])
-                            : static_cast<const float *>(scores)[pair];
-    acc = __fadd_rn(acc, __fmul_rn(TT::round(v), score));
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const uint32_t c = min(static_cast<uint32_t>(j * SW + li), cps - 1u);
+      stage.load(xl[j], src * cps + c);
+    }
+    v[s] = Sl::reduce(row_partial<TT, CPL>(rows[s], xl));
   }
-  float shared_term = 0.0f;
-  bool has_shared = false;
-  if (with_shared_expert) {
-    const ExpertPtrs e = expert_ptrs(shared.p[2], 0u, hidden, inter, group);
-    RowLoad<CPL> r;
-    load_row<CPL>(r, e, row, inter, group, li, row_ok);
-    XLane<TT> xl[CPL];
-    load_x<TT, CPL>(xl, lds_act + slots * inter, inter, li);
-    const float v = row16_sum(row_partial<TT, CPL>(r, xl));
-    shared_term = TT::round(__fmul_rn(TT::round(v), bf16_to_f32(shared_gate[token])));
-    has_shared = true;
+
+  // Padded slots (s >= keep) carry score 0 and would add exact zeros: skipped.
+  float acc = 0.0f;
+  float shared_v = 0.0f;
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const uint32_t su = static_cast<uint32_t>(s);
+    if (su < keep && slot_ok[s]) acc = __fadd_rn(acc, __fmul_rn(TT::round(v[s]), score[s]));
+    if (with_shared_expert && su == slots) shared_v = v[s];
   }
   if (li == 0 && row_ok) {
     const uint64_t idx = static_cast<uint64_t>(token) * hidden + row;
@@ -376,32 +625,47 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(
     } else if (shared_mode == kSharedParts) {
       const float comp = TT::round(__fmul_rn(TT::load(shared_vec[idx]), bf16_to_f32(shared_gate[token])));
       final_value = __fadd_rn(routed, comp);
-    } else if (has_shared) {
-      final_value = __fadd_rn(routed, shared_term);
+    } else if (with_shared_expert) {
+      final_value = __fadd_rn(routed, TT::round(__fmul_rn(TT::round(shared_v), bf16_to_f32(shared_gate[token]))));
     }
     out[idx] = TT::store(final_value);
   }
 }
 
-// ------------------------------------------------------------------ dispatch helpers
+// ------------------------------------------------------------------ dispatch
+// Slice width and chunks per lane for an input width: 64-lane slices when the
+// 32-input chunks fill the wave, otherwise 16-lane slices (tail chunks masked).
+struct Geometry {
+  int sw;
+  int cpl;
+};
 
-inline int cpl_for(uint32_t in_w) {
+inline Geometry geometry(uint32_t in_w) {
   const uint32_t chunks = in_w / 32;
-  return static_cast<int>((chunks + 15) / 16);
+  if (chunks % 64 == 0 && chunks / 64 <= 2) return {64, static_cast<int>(chunks / 64)};
+  return {16, static_cast<int>((chunks + 15) / 16)};
 }
 
-#define MQ_CPL_SWITCH(cpl, BODY)                  \
-  switch (cpl) {                                  \
-    case 1: { constexpr int CPL = 1; BODY; } break; \
-    case 2: { constexpr int CPL = 2; BODY; } break; \
-    case 3: { constexpr int CPL = 3; BODY; } break; \
-    case 4: { constexpr int CPL = 4; BODY; } break; \
-    case 5: { constexpr int CPL = 5; BODY; } break; \
-    case 6: { constexpr int CPL = 6; BODY; } break; \
-    case 7: { constexpr int CPL = 7; BODY; } break; \
-    case 8: { constexpr int CPL = 8; BODY; } break; \
-    default: return fail(MQ_ERR_UNSUPPORTED, "input width needs %d chunks per lane (max 8)", cpl); \
-  }
+#define MQ_GEOM_SWITCH(g, ...)                                                               \
+  do {                                                                                       \
+    if ((g).sw == 64 && (g).cpl == 1) { constexpr int SW = 64, CPL = 1; __VA_ARGS__; }              \
+    else if ((g).sw == 64 && (g).cpl == 2) { constexpr int SW = 64, CPL = 2; __VA_ARGS__; }         \
+    else if ((g).sw == 16 && (g).cpl == 1) { constexpr int SW = 16, CPL = 1; __VA_ARGS__; }         \
+    else if ((g).sw == 16 && (g).cpl == 2) { constexpr int SW = 16, CPL = 2; __VA_ARGS__; }         \
+    else if ((g).sw == 16 && (g).cpl == 3) { constexpr int SW = 16, CPL = 3; __VA_ARGS__; }         \
+    else if ((g).sw == 16 && (g).cpl == 4) { constexpr int SW = 16, CPL = 4; __VA_ARGS__; }         \
+    else if ((g).sw == 16 && (g).cpl == 5) { constexpr int SW = 16, CPL = 5; __VA_ARGS__; }         \
+    else if ((g).sw == 16 && (g).cpl == 6) { constexpr int SW = 16, CPL = 6; __VA_ARGS__; }         \
+    else if ((g).sw == 16 && (g).cpl == 7) { constexpr int SW = 16, CPL = 7; __VA_ARGS__; }         \
+    else if ((g).sw == 16 && (g).cpl == 8) { constexpr int SW = 16, CPL = 8; __VA_ARGS__; }         \
+    else return fail(MQ_ERR_UNSUPPORTED, "input width needs %d chunks per lane", (g).cpl);   \
+  } while (0)
+
+// Rows per wave step count: 2 steps for 64-lane slices, 1 for 16-lane slices.
+template <int SW>
+constexpr int steps_for() {
+  return SW == 64 ? 2 : 1;
+}
 
 int validate_proj(const MqProjection *p, const char *name) {
   if (p == nullptr) return fail(MQ_ERR_INVALID, "%s projection is NULL", name);
@@ -420,26 +684,88 @@ int validate_shape(uint32_t in_w, uint32_t out_w, uint32_t group) {
   if (in_w % 32) return fail(MQ_ERR_INVALID, "input width %u is not a multiple of 32", in_w);
   if (in_w > MQ_MAX_WIDTH || out_w > MQ_MAX_WIDTH * 4)
     return fail(MQ_ERR_INVALID, "projection width out of bounds (%u x %u)", out_w, in_w);
+  if (in_w / 32 > 128) return fail(MQ_ERR_UNSUPPORTED, "input width %u exceeds 4096", in_w);
+  return MQ_OK;
+}
+
+// Device error flags of the current device (allocated on first use).
+int device_flags(unsigned int **flags, hipStream_t stream) {
+  DeviceWorkspace *ws = nullptr;
+  const int rc = workspace(&ws, stream);
+  if (rc) return rc;
+  *flags = ws->flags;
   return MQ_OK;
 }
 
 template <class TT>
-int launch_gather_qmv(const void *x, int slot_input, const MqProjection &proj, const uint32_t *routes,
-                      void *out, uint32_t pairs, uint32_t slots, uint32_t in_w, uint32_t out_w,
-                      uint32_t group, hipStream_t stream) {
+int launch_gather_qmv(const void *x, int slot_input, const MqProjection &proj, const uint32_t *routes, void *out,
+                      uint32_t pairs, uint32_t slots, uint32_t in_w, uint32_t out_w, uint32_t group,
+                      uint32_t dense_count, hipStream_t stream) {
   using S = typename TT::storage;
-  const uint32_t tiles = pairs * ceil_div(out_w, kRowsPerWave);
-  const dim3 grid(ceil_div(tiles, kWaves));
-  MQ_CPL_SWITCH(cpl_for(in_w), {
-    hipLaunchKernelGGL((gather_qmv_kernel<TT, CPL>), grid, dim3(kThreads), 0, stream,
-                       static_cast<const S *>(x), slot_input, proj, routes, static_cast<S *>(out),
-                       pairs, slots, in_w, out_w, group);
+  unsigned int *err = nullptr;
+  int rc = device_flags(&err, stream);
+  if (rc) return rc;
+  const Geometry g = geometry(in_w);
+  MQ_GEOM_SWITCH(g, {
+    constexpr int R = steps_for<SW>();
+    constexpr int kTileRows = R * Slice<SW>::kRows;
+    const uint32_t tiles = pairs * ceil_div(out_w, kTileRows);
+    hipLaunchKernelGGL((gather_qmv_kernel<TT, SW, CPL, R>), dim3(ceil_div(tiles, kWaves)), dim3(kThreads), 0,
+                       stream, static_cast<const S *>(x), slot_input, proj, routes, static_cast<S *>(out), pairs,
+                       slots, in_w, out_w, group, dense_count, err);
   });
   return check_launch("gather_qmv_kernel");
 }
 
-}  // namespace
+template <class TT, bool SELECT>
+int launch_gateup(const MqMoeArgs &a, const SharedExpert &shared, bool has_shared, const int32_t *keeps,
+                  const SelectParams &sel, const SelectOutputs &sel_out, typename TT::storage *act,
+                  unsigned int *err, hipStream_t stream) {
+  using S = typename TT::storage;
+  const Geometry g = geometry(a.hidden);
+  const uint32_t pairs = a.tokens * a.slots + (has_shared ? a.tokens : 0u);
+  MQ_GEOM_SWITCH(g, {
+    constexpr int R = steps_for<SW>();
+    constexpr int kTileRows = R * Slice<SW>::kRows;
+    const uint32_t tiles = pairs * ceil_div(a.inter, kTileRows);
+    hipLaunchKernelGGL((gateup_kernel<TT, SW, CPL, R, SELECT>), dim3(ceil_div(tiles, kWaves)), dim3(kThreads), 0,
+                       stream, static_cast<const S *>(a.x), a.gate, a.up, shared, has_shared, a.routes, keeps, sel,
+                       sel_out, act, static_cast<S *>(a.gate_out), static_cast<S *>(a.up_out), a.tokens, a.slots,
+                       a.hidden, a.inter, a.group_size, a.expert_count, tiles, err);
+  });
+  return check_launch("gateup_kernel");
+}
 
+template <class TT, int SW, int CPL, int NS>
+void launch_down_ns(const MqMoeArgs &a, const SharedExpert &shared, int shared_mode,
+                    const typename TT::storage *shared_vec, const int32_t *keeps, const typename TT::storage *act,
+                    unsigned int *err, size_t lds, hipStream_t stream) {
+  using S = typename TT::storage;
+  const uint32_t tiles_per_token = ceil_div(a.hidden, Slice<SW>::kRows);
+  const dim3 grid(ceil_div(tiles_per_token, kWaves), a.tokens);
+  hipLaunchKernelGGL((down_combine_kernel<TT, SW, CPL, NS>), grid, dim3(kThreads), lds, stream, act, a.down, shared,
+                     a.routes, a.scores, a.score_dtype, keeps, shared_mode, shared_vec, a.shared_gate,
+                     static_cast<S *>(a.out), a.tokens, a.slots, a.hidden, a.inter, a.group_size, tiles_per_token,
+                     a.expert_count, err);
+}
+
+template <class TT>
+int launch_down(const MqMoeArgs &a, const SharedExpert &shared, int shared_mode, const typename TT::storage *shared_vec,
+                const int32_t *keeps, const typename TT::storage *act, unsigned int *err, hipStream_t stream) {
+  const Geometry g = geometry(a.inter);
+  const uint32_t n_src = a.slots + (shared_mode == kSharedExpert ? 1u : 0u);
+  const size_t lds = static_cast<size_t>(n_src) * (a.inter / 32) * StagedX<TT>::kBytesPerChunk;
+  if (lds > 64 * 1024) return fail(MQ_ERR_UNSUPPORTED, "activation staging needs %zu bytes of LDS", lds);
+  MQ_GEOM_SWITCH(g, {
+    if (n_src <= 4) launch_down_ns<TT, SW, CPL, 4>(a, shared, shared_mode, shared_vec, keeps, act, err, lds, stream);
+    else if (n_src <= 8) launch_down_ns<TT, SW, CPL, 8>(a, shared, shared_mode, shared_vec, keeps, act, err, lds, stream);
+    else if (n_src <= 12) launch_down_ns<TT, SW, CPL, 12>(a, shared, shared_mode, shared_vec, keeps, act, err, lds, stream);
+    else launch_down_ns<TT, SW, CPL, 17>(a, shared, shared_mode, shared_vec, keeps, act, err, lds, stream);
+  });
+  return check_launch("down_combine_kernel");
+}
+
+}  // namespace
 }  // namespace mq
 
 using namespace mq;
@@ -448,20 +774,20 @@ extern "C" int mq_gather_qmv(const void *x, int x_dtype, int slot_input, const M
                              const uint32_t *routes, void *out, uint32_t tokens, uint32_t slots,
                              uint32_t in_features, uint32_t out_features, uint32_t expert_count,
                              uint32_t group_size, void *stream) {
-  if (x == nullptr || out == nullptr || routes == nullptr) return fail(MQ_ERR_INVALID, "x, routes and out are required");
+  if (x == nullptr || out == nullptr || routes == nullptr)
+    return fail(MQ_ERR_INVALID, "x, routes and out are required");
   int rc = validate_proj(proj, "gather");
   if (rc) return rc;
   if ((rc = validate_shape(in_features, out_features, group_size))) return rc;
   if (tokens == 0 || slots == 0) return fail(MQ_ERR_INVALID, "tokens and slots must be positive");
-  (void)expert_count;
   const uint32_t pairs = tokens * slots;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (x_dtype == MQ_BF16)
-    return launch_gather_qmv<BF16T>(x, slot_input, *proj, routes, out, pairs, slots, in_features,
-                                    out_features, group_size, s);
+    return launch_gather_qmv<BF16T>(x, slot_input, *proj, routes, out, pairs, slots, in_features, out_features,
+                                    group_size, expert_count, s);
   if (x_dtype == MQ_F32)
-    return launch_gather_qmv<F32T>(x, slot_input, *proj, routes, out, pairs, slots, in_features,
-                                   out_features, group_size, s);
+    return launch_gather_qmv<F32T>(x, slot_input, *proj, routes, out, pairs, slots, in_features, out_features,
+                                   group_size, expert_count, s);
   return fail(MQ_ERR_INVALID, "x_dtype must be MQ_BF16 or MQ_F32");
 }
 
@@ -480,11 +806,9 @@ extern "C" int mq_q4_qmv(const void *x, int x_dtype, const uint32_t *weight, con
   hipStream_t s = static_cast<hipStream_t>(stream);
   // One "pair" per activation row, all addressing expert 0 (routes == NULL).
   if (x_dtype == MQ_BF16)
-    return launch_gather_qmv<BF16T>(x, 0, p, nullptr, y, rows_x, 1, in_features, out_features,
-                                    group_size, s);
+    return launch_gather_qmv<BF16T>(x, 0, p, nullptr, y, rows_x, 1, in_features, out_features, group_size, 1u, s);
   if (x_dtype == MQ_F32)
-    return launch_gather_qmv<F32T>(x, 0, p, nullptr, y, rows_x, 1, in_features, out_features,
-                                   group_size, s);
+    return launch_gather_qmv<F32T>(x, 0, p, nullptr, y, rows_x, 1, in_features, out_features, group_size, 1u, s);
   return fail(MQ_ERR_INVALID, "x_dtype must be MQ_BF16 or MQ_F32");
 }
 
@@ -492,14 +816,18 @@ namespace mq {
 namespace {
 
 template <class TT>
-int moe_decode_t(const MqMoeArgs &a, hipStream_t stream) {
+int moe_decode_t(const MqMoeArgs &a, hipStream_t stream, const MqRouteArgs *route, const uint16_t *logits) {
   using S = typename TT::storage;
   const uint32_t routed_pairs = a.tokens * a.slots;
   const bool return_all = (a.flags & MQ_DECODE_RETURN_ALL) != 0;
   const bool has_shared_expert = a.shared_expert != nullptr && !return_all;
   const uint32_t pairs = routed_pairs + (has_shared_expert ? a.tokens : 0u);
 
-  // Activations: caller buffer or a library scratch buffer.
+  unsigned int *err = nullptr;
+  int rc = device_flags(&err, stream);
+  if (rc) return rc;
+
+  // Activations: caller buffer or a grow-only library scratch buffer.
   S *act = static_cast<S *>(a.act_out);
   static thread_local void *scratch = nullptr;
   static thread_local size_t scratch_bytes = 0;
@@ -509,6 +837,9 @@ int moe_decode_t(const MqMoeArgs &a, hipStream_t stream) {
   const size_t need = static_cast<size_t>(pairs) * a.inter * sizeof(S);
   if (act == nullptr) {
     if (scratch == nullptr || scratch_bytes < need || scratch_dev != device) {
+      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+      if (stream != nullptr && hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
+        return fail(MQ_ERR_INVALID, "pass act_out when decoding inside graph capture");
       if (scratch != nullptr && scratch_dev == device) {
         MQ_TRY_HIP(hipDeviceSynchronize());
         (void)hipFree(scratch);
@@ -521,54 +852,65 @@ int moe_decode_t(const MqMoeArgs &a, hipStream_t stream) {
     act = static_cast<S *>(scratch);
   }
 
-  SharedExpert shared_dev{};
-  if (has_shared_expert) {
-    for (int i = 0; i < 3; ++i) shared_dev.p[i] = a.shared_expert[i];
-  }
+  SharedExpert shared{};
+  if (has_shared_expert)
+    for (int i = 0; i < 3; ++i) shared.p[i] = a.shared_expert[i];
   const int32_t *keeps = return_all ? nullptr : a.keeps;
+  const uint32_t ne = a.expert_count;
 
-  if (a.flags & MQ_DECODE_UNFUSED_UP) {
+  if (route != nullptr) {
+    // Fused routed layer: the gate/up kernel runs the selection itself.
+    SelectOutputs so{};
+    so.inds = route->inds;
+    so.scores = static_cast<uint16_t *>(route->scores);
+    so.scores_raw = route->scores_raw;
+    so.routes = route->routes;
+    so.keeps = route->keeps;
+    so.shared_gate = route->shared_gate;
+    so.shared_logit = route->shared_gate;
+    const SelectParams sel = select_params(*route, logits);
+    rc = launch_gateup<TT, true>(a, shared, has_shared_expert, nullptr, sel, so, act, err, stream);
+    if (rc) return rc;
+    keeps = route->threshold < 1.0f ? route->keeps : nullptr;
+  } else if (a.flags & MQ_DECODE_UNFUSED_UP) {
     // Separate gate/up QMVs then SwiGLU: bit-identical to the fused kernel.
     S *g = static_cast<S *>(a.gate_out);
     S *u = static_cast<S *>(a.up_out);
-    if (g == nullptr || u == nullptr)
-      return fail(MQ_ERR_INVALID, "unfused up path needs gate_out and up_out buffers");
-    int rc = launch_gather_qmv<TT>(a.x, 0, a.gate, a.routes, g, routed_pairs, a.slots, a.hidden,
-                                   a.inter, a.group_size, stream);
+    if (g == nullptr || u == nullptr) return fail(MQ_ERR_INVALID, "unfused up path needs gate_out and up_out buffers");
+    rc = launch_gather_qmv<TT>(a.x, 0, a.gate, a.routes, g, routed_pairs, a.slots, a.hidden, a.inter, a.group_size,
+                               ne, stream);
     if (rc) return rc;
-    rc = launch_gather_qmv<TT>(a.x, 0, a.up, a.routes, u, routed_pairs, a.slots, a.hidden, a.inter,
-                               a.group_size, stream);
+    rc = launch_gather_qmv<TT>(a.x, 0, a.up, a.routes, u, routed_pairs, a.slots, a.hidden, a.inter, a.group_size,
+                               ne, stream);
     if (rc) return rc;
     const uint64_t n = static_cast<uint64_t>(routed_pairs) * a.inter;
     hipLaunchKernelGGL(swiglu_kernel<TT>, dim3(ceil_div(n, 256)), dim3(256), 0, stream, g, u, act, n);
     if ((rc = check_launch("swiglu_kernel"))) return rc;
     if (has_shared_expert) {
-      // Shared pairs follow the routed pairs: pair_base = tokens * slots.
-      const uint32_t tiles = a.tokens * ceil_div(a.inter, kRowsPerWave);
-      MQ_CPL_SWITCH(cpl_for(a.hidden), {
-        hipLaunchKernelGGL((gateup_swiglu_kernel<TT, CPL>), dim3(ceil_div(tiles, kWaves)), dim3(kThreads), 0,
-                           stream, static_cast<const S *>(a.x), a.gate, a.up, shared_dev, a.routes,
-                           keeps, act, nullptr, nullptr, a.tokens, a.slots, routed_pairs, a.tokens,
-                           a.hidden, a.inter, a.group_size);
+      // Only the shared pairs (the routed pairs were computed above): the
+      // shared tiles come first, so a tile limit of `shared tiles` covers them.
+      const Geometry g2 = geometry(a.hidden);
+      MQ_GEOM_SWITCH(g2, {
+        constexpr int R = steps_for<SW>();
+        constexpr int kTileRows = R * Slice<SW>::kRows;
+        const uint32_t tiles = a.tokens * ceil_div(a.inter, kTileRows);
+        hipLaunchKernelGGL((gateup_kernel<TT, SW, CPL, R, false>), dim3(ceil_div(tiles, kWaves)), dim3(kThreads), 0,
+                           stream, static_cast<const S *>(a.x), a.gate, a.up, shared, true, a.routes, keeps,
+                           SelectParams{}, SelectOutputs{}, act, nullptr, nullptr, a.tokens, a.slots, a.hidden,
+                           a.inter, a.group_size, ne, tiles, err);
       });
-      if ((rc = check_launch("gateup_swiglu_kernel"))) return rc;
+      if ((rc = check_launch("gateup_kernel"))) return rc;
     }
   } else {
-    const uint32_t tiles = pairs * ceil_div(a.inter, kRowsPerWave);
-    MQ_CPL_SWITCH(cpl_for(a.hidden), {
-      hipLaunchKernelGGL((gateup_swiglu_kernel<TT, CPL>), dim3(ceil_div(tiles, kWaves)), dim3(kThreads), 0,
-                         stream, static_cast<const S *>(a.x), a.gate, a.up, shared_dev, a.routes, keeps,
-                         act, static_cast<S *>(a.gate_out), static_cast<S *>(a.up_out), a.tokens, a.slots,
-                         0u, pairs, a.hidden, a.inter, a.group_size);
-    });
-    int rc = check_launch("gateup_swiglu_kernel");
+    rc = launch_gateup<TT, false>(a, shared, has_shared_expert, keeps, SelectParams{}, SelectOutputs{}, act, err,
+                                  stream);
     if (rc) return rc;
   }
 
   if (return_all) {
     if (a.down_out == nullptr) return fail(MQ_ERR_INVALID, "return_all needs down_out");
-    return launch_gather_qmv<TT>(act, 1, a.down, a.routes, a.down_out, routed_pairs, a.slots, a.inter,
-                                 a.hidden, a.group_size, stream);
+    return launch_gather_qmv<TT>(act, 1, a.down, a.routes, a.down_out, routed_pairs, a.slots, a.inter, a.hidden,
+                                 a.group_size, ne, stream);
   }
 
   int shared_mode = kSharedNone;
@@ -582,17 +924,33 @@ int moe_decode_t(const MqMoeArgs &a, hipStream_t stream) {
   } else if (has_shared_expert) {
     shared_mode = kSharedExpert;
   }
-  const uint32_t tiles_per_token = ceil_div(a.hidden, kRowsPerWave);
-  const dim3 grid(ceil_div(tiles_per_token, kWaves), a.tokens);
-  const size_t lds = static_cast<size_t>(a.slots + 1) * a.inter * sizeof(S);
-  if (lds > 160 * 1024) return fail(MQ_ERR_UNSUPPORTED, "activation staging needs %zu bytes of LDS", lds);
-  MQ_CPL_SWITCH(cpl_for(a.inter), {
-    hipLaunchKernelGGL((down_combine_kernel<TT, CPL>), grid, dim3(kThreads), lds, stream, act, a.down,
-                       shared_dev, a.routes, a.scores, a.score_dtype, keeps, shared_mode, shared_vec,
-                       a.shared_gate, static_cast<S *>(a.out), a.tokens, a.slots, a.hidden, a.inter,
-                       a.group_size, tiles_per_token);
-  });
-  return check_launch("down_combine_kernel");
+  return launch_down<TT>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+}
+
+int validate_moe_args(const MqMoeArgs &a, bool routed_layer) {
+  if (a.x == nullptr) return fail(MQ_ERR_INVALID, "x is required");
+  if (!routed_layer && a.routes == nullptr) return fail(MQ_ERR_INVALID, "x and routes are required");
+  if (a.tokens == 0 || a.tokens > 64) return fail(MQ_ERR_INVALID, "tokens must be in 1..64 (got %u)", a.tokens);
+  if (a.slots == 0 || a.slots > kMaxSlots) return fail(MQ_ERR_INVALID, "slots must be in 1..16 (got %u)", a.slots);
+  int rc;
+  if ((rc = validate_proj(&a.gate, "gate")) || (rc = validate_proj(&a.up, "up")) || (rc = validate_proj(&a.down, "down")))
+    return rc;
+  if ((rc = validate_shape(a.hidden, a.inter, a.group_size)) || (rc = validate_shape(a.inter, a.hidden, a.group_size)))
+    return rc;
+  const bool return_all = (a.flags & MQ_DECODE_RETURN_ALL) != 0;
+  if (!return_all) {
+    if (!routed_layer && a.scores == nullptr) return fail(MQ_ERR_INVALID, "scores are required unless return_all is set");
+    if (a.out == nullptr) return fail(MQ_ERR_INVALID, "out is required");
+    if (a.score_dtype != MQ_F32 && a.score_dtype != MQ_BF16) return fail(MQ_ERR_INVALID, "bad score dtype");
+    const int modes = (a.shared_y != nullptr) + (a.shared != nullptr) + (a.shared_expert != nullptr);
+    if (modes > 1) return fail(MQ_ERR_INVALID, "provide shared_y, shared parts or a shared expert, not several");
+    if ((a.shared != nullptr || a.shared_expert != nullptr) && a.shared_gate == nullptr)
+      return fail(MQ_ERR_INVALID, "shared and shared_gate must be provided together");
+    if (a.shared_expert != nullptr)
+      for (int i = 0; i < 3; ++i)
+        if ((rc = validate_proj(&a.shared_expert[i], "shared"))) return rc;
+  }
+  return MQ_OK;
 }
 
 }  // namespace
@@ -601,32 +959,39 @@ int moe_decode_t(const MqMoeArgs &a, hipStream_t stream) {
 extern "C" int mq_moe_decode(const MqMoeArgs *args, void *stream) {
   if (args == nullptr) return fail(MQ_ERR_INVALID, "args is NULL");
   const MqMoeArgs &a = *args;
-  if (a.x == nullptr || a.routes == nullptr) return fail(MQ_ERR_INVALID, "x and routes are required");
-  if (a.tokens == 0 || a.tokens > 64) return fail(MQ_ERR_INVALID, "tokens must be in 1..64 (got %u)", a.tokens);
-  if (a.slots == 0 || a.slots > 16) return fail(MQ_ERR_INVALID, "slots must be in 1..16 (got %u)", a.slots);
-  int rc;
-  if ((rc = validate_proj(&a.gate, "gate")) || (rc = validate_proj(&a.up, "up")) ||
-      (rc = validate_proj(&a.down, "down")))
-    return rc;
-  if ((rc = validate_shape(a.hidden, a.inter, a.group_size)) ||
-      (rc = validate_shape(a.inter, a.hidden, a.group_size)))
-    return rc;
-  const bool return_all = (a.flags & MQ_DECODE_RETURN_ALL) != 0;
-  if (!return_all) {
-    if (a.scores == nullptr) return fail(MQ_ERR_INVALID, "scores are required unless return_all is set");
-    if (a.out == nullptr) return fail(MQ_ERR_INVALID, "out is required");
-    if (a.score_dtype != MQ_F32 && a.score_dtype != MQ_BF16) return fail(MQ_ERR_INVALID, "bad score dtype");
-    const int modes = (a.shared_y != nullptr) + (a.shared != nullptr) + (a.shared_expert != nullptr);
-    if (modes > 1) return fail(MQ_ERR_INVALID, "provide shared_y, shared parts or a shared expert, not several");
-    if ((a.shared != nullptr || a.shared_expert != nullptr) && a.shared_gate == nullptr)
-      return fail(MQ_ERR_INVALID, "shared and shared_gate must be provided together");
-    if (a.shared_expert != nullptr) {
-      for (int i = 0; i < 3; ++i)
-        if ((rc = validate_proj(&a.shared_expert[i], "shared"))) return rc;
-    }
-  }
+  int rc = validate_moe_args(a, false);
+  if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (a.x_dtype == MQ_BF16) return moe_decode_t<BF16T>(a, s);
-  if (a.x_dtype == MQ_F32) return moe_decode_t<F32T>(a, s);
+  if (a.x_dtype == MQ_BF16) return moe_decode_t<BF16T>(a, s, nullptr, nullptr);
+  if (a.x_dtype == MQ_F32) return moe_decode_t<F32T>(a, s, nullptr, nullptr);
   return fail(MQ_ERR_INVALID, "x_dtype must be MQ_BF16 or MQ_F32");
+}
+
+extern "C" int mq_moe_layer(const MqRouteArgs *route, const MqMoeArgs *moe, void *stream) {
+  if (route == nullptr || moe == nullptr) return fail(MQ_ERR_INVALID, "route and moe args are required");
+  const MqRouteArgs &r = *route;
+  MqMoeArgs a = *moe;
+  int rc = validate_route_args(r);
+  if (rc) return rc;
+  if (r.logits_in != nullptr || r.logits_out == nullptr || r.routes == nullptr || r.x == nullptr)
+    return fail(MQ_ERR_INVALID, "the routed layer needs x, gate_w, logits_out and routes (no logits_in)");
+  if (r.score_dtype != MQ_BF16) return fail(MQ_ERR_INVALID, "the routed layer produces bf16 scores");
+  if (moe->x_dtype != MQ_BF16 || moe->x != r.x) return fail(MQ_ERR_INVALID, "the routed layer needs the same bf16 x");
+  if (r.tokens != moe->tokens || r.top_k != moe->slots || r.hidden != moe->hidden)
+    return fail(MQ_ERR_INVALID, "route and moe shapes disagree");
+  if (r.tokens > kMaxLayerTokens) return fail(MQ_ERR_INVALID, "the routed layer handles at most %u tokens", kMaxLayerTokens);
+  if (moe->flags != 0) return fail(MQ_ERR_INVALID, "the routed layer supports no MQ_DECODE flags");
+  if ((moe->shared_expert != nullptr) != (r.shared_gate != nullptr))
+    return fail(MQ_ERR_INVALID, "a shared expert needs the router's shared_gate output and vice versa");
+  a.routes = r.routes;
+  a.scores = r.scores;
+  a.score_dtype = MQ_BF16;
+  a.shared_gate = r.shared_gate;
+  a.keeps = r.keeps;
+  if ((rc = validate_moe_args(a, true))) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  rc = launch_router_logits(r.x, r.gate_w, r.shared_gate != nullptr ? r.shared_gate_w : nullptr, r.logits_out,
+                            r.shared_gate, r.tokens, r.hidden, r.experts, s);
+  if (rc) return rc;
+  return moe_decode_t<BF16T>(a, s, &r, r.logits_out);
 }

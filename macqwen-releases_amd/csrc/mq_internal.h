@@ -25,7 +25,9 @@ struct DeviceWorkspace {
   unsigned int *flags;     // error flags set by bounded waits
 };
 constexpr int kCounterSlots = 64;
-int workspace(DeviceWorkspace **out);
+// The current device's workspace; allocates it on first use unless `stream`
+// is capturing a graph (then the call fails and asks for mq_init()).
+int workspace(DeviceWorkspace **out, hipStream_t stream);
 
 // ---------------------------------------------------------------- bf16
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
@@ -139,6 +141,57 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, 0xf, 0xf, false));
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = dpp_u<CTRL>(static_cast<uint32_t>(u));
+  const uint32_t hi = dpp_u<CTRL>(static_cast<uint32_t>(u >> 32));
+  return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ uint32_t readlane_u(uint32_t v, int lane) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
+}
+
+__device__ __forceinline__ double readlane_d(double v, int lane) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint64_t lo = readlane_u(static_cast<uint32_t>(u), lane);
+  const uint64_t hi = readlane_u(static_cast<uint32_t>(u >> 32), lane);
+  return __builtin_bit_cast(double, (hi << 32) | lo);
+}
+
+// Wave-uniform max of unsigned keys (all 64 lanes active).
+__device__ __forceinline__ uint32_t wave_max_u32_uniform(uint32_t v) {
+  v = max(v, dpp_u<0xb1>(v));
+  v = max(v, dpp_u<0x4e>(v));
+  v = max(v, dpp_u<0x124>(v));
+  v = max(v, dpp_u<0x128>(v));
+  return max(max(readlane_u(v, 0), readlane_u(v, 16)), max(readlane_u(v, 32), readlane_u(v, 48)));
+}
+
+// Wave-uniform float64 max and sum (all 64 lanes active).  The sum order is
+// fixed: quads, then rows of 16, then the four rows.
+__device__ __forceinline__ double wave_max_f64_uniform(double v) {
+  v = fmax(v, dpp_d<0xb1>(v));
+  v = fmax(v, dpp_d<0x4e>(v));
+  v = fmax(v, dpp_d<0x124>(v));
+  v = fmax(v, dpp_d<0x128>(v));
+  return fmax(fmax(readlane_d(v, 0), readlane_d(v, 16)), fmax(readlane_d(v, 32), readlane_d(v, 48)));
+}
+
+__device__ __forceinline__ double wave_sum_f64_uniform(double v) {
+  v += dpp_d<0xb1>(v);
+  v += dpp_d<0x4e>(v);
+  v += dpp_d<0x124>(v);
+  v += dpp_d<0x128>(v);
+  return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
   return v;
@@ -157,32 +210,44 @@ struct ExpertPtrs {
   const uint32_t *w;
   const uint16_t *s;
   const uint16_t *b;
+  bool ok;  // false: the word addresses no valid record; nothing may be read
 };
 
 // Resolve a route word to the rows of one projection
-// (models/flashnext/metal_runtime.py:194-228; 64-bit pool offsets).
+// (models/flashnext/metal_runtime.py:194-228; 64-bit pool offsets).  Words
+// are bound-checked against the record or expert counts.
 __device__ __forceinline__ ExpertPtrs expert_ptrs(const MqProjection &p, uint32_t word,
                                                   uint32_t out_w, uint32_t in_w,
-                                                  uint32_t group) {
-  ExpertPtrs r;
+                                                  uint32_t group, uint32_t dense_count) {
+  ExpertPtrs r{nullptr, nullptr, nullptr, false};
+  const uint8_t *rec = nullptr;
   if (word & MQ_SLOT_BIT) {
-    const uint8_t *rec = p.pool + p.pool_header +
-                         static_cast<uint64_t>(word & 0x7fffffffu) * p.pool_stride;
-    r.w = reinterpret_cast<const uint32_t *>(rec + p.off_weight);
-    r.s = reinterpret_cast<const uint16_t *>(rec + p.off_scales);
-    r.b = reinterpret_cast<const uint16_t *>(rec + p.off_biases);
+    const uint32_t slot = word & 0x7fffffffu;
+    if (p.pool != nullptr && slot < p.pool_slots)
+      rec = p.pool + p.pool_header + static_cast<uint64_t>(slot) * p.pool_stride;
   } else if (p.stream_pack != nullptr) {
-    const uint8_t *rec = p.stream_pack + static_cast<uint64_t>(word) * p.pool_stride;
-    r.w = reinterpret_cast<const uint32_t *>(rec + p.off_weight);
-    r.s = reinterpret_cast<const uint16_t *>(rec + p.off_scales);
-    r.b = reinterpret_cast<const uint16_t *>(rec + p.off_biases);
-  } else {
+    if (word < p.stream_records) rec = p.stream_pack + static_cast<uint64_t>(word) * p.pool_stride;
+  } else if (p.weight != nullptr && word < dense_count) {
     const uint64_t e = word;
     r.w = p.weight + e * out_w * (in_w / 8);
     r.s = p.scales + e * out_w * (in_w / group);
     r.b = p.biases + e * out_w * (in_w / group);
+    r.ok = true;
+    return r;
+  }
+  if (rec != nullptr) {
+    r.w = reinterpret_cast<const uint32_t *>(rec + p.off_weight);
+    r.s = reinterpret_cast<const uint16_t *>(rec + p.off_scales);
+    r.b = reinterpret_cast<const uint16_t *>(rec + p.off_biases);
+    r.ok = true;
   }
   return r;
+}
+
+// Raise a device error flag (vector atomic from one lane).
+__device__ __forceinline__ void raise_flag(unsigned int *flags, unsigned int bit) {
+  if (flags != nullptr)
+    __hip_atomic_fetch_or(flags, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- host helpers

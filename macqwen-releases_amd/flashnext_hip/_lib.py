@@ -28,9 +28,10 @@ MQ_DECODE_UNFUSED_UP = 2
 
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTS = (
-    "mq_available", "mq_last_error", "mq_version", "mq_record_layout",
+    "mq_available", "mq_init", "mq_last_error", "mq_check_device_errors", "mq_version",
+    "mq_abi_struct_size", "mq_record_layout",
     "mq_q4_unpack", "mq_q4_dequant", "mq_q4_qmv", "mq_gather_qmv",
-    "mq_route_topk", "mq_moe_decode", "mq_grouped_workspace_size",
+    "mq_route_topk", "mq_moe_decode", "mq_moe_layer", "mq_grouped_workspace_size",
     "mq_moe_grouped", "mq_pool_refill_async",
 )
 
@@ -59,6 +60,8 @@ class MqProjection(ctypes.Structure):
         ("off_scales", ctypes.c_uint64),
         ("off_biases", ctypes.c_uint64),
         ("stream_pack", ctypes.c_void_p),
+        ("pool_slots", ctypes.c_uint32),
+        ("stream_records", ctypes.c_uint32),
     ]
 
 
@@ -149,8 +152,11 @@ def _declare(lib) -> None:
     vp, u32, u64, i32 = c.c_void_p, c.c_uint32, c.c_uint64, c.c_int
     sig = {
         "mq_available": ([], i32),
+        "mq_init": ([], i32),
         "mq_last_error": ([c.c_char_p, u32], i32),
+        "mq_check_device_errors": ([vp, c.POINTER(c.c_uint32)], i32),
         "mq_version": ([], i32),
+        "mq_abi_struct_size": ([i32], u64),
         "mq_record_layout": ([u32, u32, u32, c.POINTER(c.c_uint64), c.POINTER(c.c_uint64)], i32),
         "mq_q4_unpack": ([vp, vp, u64, vp], i32),
         "mq_q4_dequant": ([vp, vp, vp, vp, u32, u32, u32, vp], i32),
@@ -158,6 +164,7 @@ def _declare(lib) -> None:
         "mq_gather_qmv": ([vp, i32, i32, c.POINTER(MqProjection), vp, vp, u32, u32, u32, u32, u32, u32, vp], i32),
         "mq_route_topk": ([c.POINTER(MqRouteArgs), vp], i32),
         "mq_moe_decode": ([c.POINTER(MqMoeArgs), vp], i32),
+        "mq_moe_layer": ([c.POINTER(MqRouteArgs), c.POINTER(MqMoeArgs), vp], i32),
         "mq_grouped_workspace_size": ([u32, u32, u32, u32, u32], u64),
         "mq_moe_grouped": ([c.POINTER(MqGroupedArgs), vp], i32),
         "mq_pool_refill_async": ([vp, u64, u64, vp, vp, u32, u64, vp, vp], i32),
@@ -183,9 +190,24 @@ def load(path: str | os.PathLike | None = None):
         _LOAD_ERROR = f"cannot load {target}: {exc}"
         raise NativeUnavailable(_LOAD_ERROR) from exc
     _declare(lib)
+    for which, struct in enumerate((MqProjection, MqMoeArgs, MqRouteArgs, MqGroupedArgs)):
+        native = int(lib.mq_abi_struct_size(which))
+        if native != ctypes.sizeof(struct):
+            _LOAD_ERROR = (f"{target} is out of date: sizeof({struct.__name__}) is {native} in the "
+                           f"library but {ctypes.sizeof(struct)} in the binding; rebuild it")
+            raise NativeUnavailable(_LOAD_ERROR)
     if path is None:
         _LIB = lib
+        init_device()
     return lib
+
+
+def init_device() -> None:
+    """Allocate the library workspace on the current device (before any graph
+    capture); a no-op when no gfx950 device is visible."""
+    lib = _LIB
+    if lib is not None and lib.mq_available() == 1:
+        check(lib.mq_init(), lib)
 
 
 def last_error(lib=None) -> str:
@@ -205,6 +227,14 @@ def check(rc: int, lib=None) -> None:
     if rc == MQ_ERR_DEVICE:
         raise NativeUnavailable(message)
     raise NativeError(rc, message)
+
+
+def check_device_errors(stream=None) -> int:
+    """Synchronise ``stream`` and raise if a kernel flagged a bad route word."""
+    lib = load()
+    flags = ctypes.c_uint32(0)
+    check(lib.mq_check_device_errors(stream, ctypes.byref(flags)), lib)
+    return int(flags.value)
 
 
 def record_layout(hidden: int, inter: int, group_size: int = 32):

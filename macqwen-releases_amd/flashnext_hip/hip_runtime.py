@@ -173,6 +173,10 @@ def _projection_struct(proj: Q4G32Projection | None, pool=None, stream_pack=None
         p.stream_pack = ptr(stream_pack) if stream_pack is not None else None
         p.pool_header = HEADER_SIZE
         p.pool_stride = layout.record_stride
+        if pool is not None:
+            p.pool_slots = max(0, (pool.numel() * pool.element_size() - HEADER_SIZE) // layout.record_stride)
+        if stream_pack is not None:
+            p.stream_records = (stream_pack.numel() * stream_pack.element_size()) // layout.record_stride
         p.off_weight = layout.offset(name, "weight")
         p.off_scales = layout.offset(name, "scales")
         p.off_biases = layout.offset(name, "biases")
@@ -328,7 +332,9 @@ class HipMoEExecutor:
         args.down = _projection_struct(down, slab_pack, stream_pack, layout, "down_proj")
         args.routes = ptr(route_words)
         args.tokens, args.slots, args.hidden, args.inter = tokens, slots, hidden, inter
-        args.expert_count, args.group_size = self.expert_count, self.group_size
+        # Dense route words are bounded by the bank the arrays actually hold.
+        args.expert_count = min(int(_shape(w.weight)[0]) for w in (gate, up, down))
+        args.group_size = self.group_size
         keep_alive = [route_words]
 
         g64_generic = scores is not None and not return_all and self.group_size == 64

@@ -28,6 +28,7 @@ def pool_projection(pool: torch.Tensor, layout: SlabLayout, name: str) -> _lib.M
     p.off_weight = layout.offset(name, "weight")
     p.off_scales = layout.offset(name, "scales")
     p.off_biases = layout.offset(name, "biases")
+    p.pool_slots = (pool.numel() * pool.element_size() - HEADER_SIZE) // layout.record_stride
     return p
 
 
@@ -99,14 +100,16 @@ class DecodeLayer:
         self._lib = _lib.load()
 
     def launch(self, stream: int | None) -> None:
-        """Route + experts on ``stream`` (a raw hipStream_t handle)."""
-        lib = self._lib
-        rc = lib.mq_route_topk(self.route_args, stream)
+        """The whole layer on ``stream`` (a raw hipStream_t handle): router
+        logits, gate/up with the top-k selection folded in, down + combine."""
+        rc = self._lib.mq_moe_layer(self.route_args, self.moe_args, stream)
         if rc:
-            _lib.check(rc, lib)
-        rc = lib.mq_moe_decode(self.moe_args, stream)
-        if rc:
-            _lib.check(rc, lib)
+            _lib.check(rc, self._lib)
+
+    def launch_unfused(self, stream) -> None:
+        """Same layer as separate router (logits + select) and expert calls."""
+        self.launch_router(stream)
+        self.launch_experts(stream)
 
     def launch_router(self, stream):
         _lib.check(self._lib.mq_route_topk(self.route_args, stream), self._lib)

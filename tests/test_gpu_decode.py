@@ -295,6 +295,72 @@ def test_pool_and_stream_pack_addressing_bit_identical(torch_mod, records, dev_r
     assert torch.equal(dense.view(torch.int16), streamed.view(torch.int16))
 
 
+@pytest.mark.parametrize("tokens,threshold", [(1, 1.0), (4, 1.0), (8, 0.85)])
+def test_fused_routed_layer_matches_unfused_and_oracle(torch_mod, records, shared_records, tokens, threshold):
+    torch = torch_mod
+    say(f"case: fused routed layer tokens={tokens} threshold={threshold}")
+    from flashnext_hip.layout import make_layout
+    from flashnext_hip.moe_block import DecodeLayer, LayerWeights
+
+    slots = 24
+    perm = np.random.default_rng(160).permutation(slots)[:E].astype(np.int32)
+    img, _ = pool_from_banks(records, perm, slots, H, I)
+    wg = bf16_normal((E, H), seed=161, std=0.02)
+    wsg = bf16_normal((1, H), seed=162, std=0.02)
+    sh = tuple(tuple(t[:1] for t in to_dev_bank(b)) for b in (shared_records.gate, shared_records.up,
+                                                               shared_records.down))
+    weights = LayerWeights(make_layout(H, I), torch.from_numpy(img).cuda(), torch.from_numpy(perm).cuda(),
+                           to_dev_bf16(wg), to_dev_bf16(wsg).reshape(-1), sh)
+    layer = DecodeLayer(weights, tokens, 10, threshold=threshold, min_keep=2)
+    x = bf16_normal((tokens, H), seed=163)
+    layer.x.copy_(to_dev_bf16(x))
+    layer.launch(None)
+    torch.cuda.synchronize()
+    fused = layer.out.clone()
+    fused_routes = layer.routes.clone()
+    layer.launch_unfused(None)
+    torch.cuda.synchronize()
+    assert torch.equal(fused_routes, layer.routes)
+    assert torch.equal(fused.view(torch.int16), layer.out.view(torch.int16))
+    from flashnext_hip import _lib
+
+    assert _lib.check_device_errors() == 0
+    ref = orouter.route(x, wg, 10, threshold=threshold, min_keep=2, slot_table=perm.astype(np.uint32))
+    assert np.array_equal(layer.inds.cpu().numpy().astype(np.uint32), ref["inds"])
+    assert np.array_equal(layer.routes.cpu().numpy().view(np.uint32), ref["routes"])
+    recs = moe.ExpertRecordSet(records.gate, records.up, records.down,
+                               shared=(shared_records.gate, shared_records.up, shared_records.down))
+    want = moe.decode_layer(x, ref["inds"], ref["scores"], recs, score_dtype="bf16", shared_gate_weight=wsg,
+                            keeps=ref["keeps"] if threshold < 1 else None)
+    assert_close(bf16.bf16_to_f32(from_dev_bf16(fused)), bf16.bf16_to_f32(want), "fused routed layer")
+
+
+def test_out_of_range_route_word_is_skipped_and_flagged(torch_mod, records, dev_records):
+    torch = torch_mod
+    say("case: slot word beyond the pool is bound-checked in-kernel")
+    from flashnext_hip import _lib
+
+    _lib.check_device_errors()  # start clean
+    x = to_dev_bf16(bf16_normal((1, H), seed=115))
+    slots = 4
+    img, _stride = pool_from_banks(records, np.arange(slots), slots, H, I)
+    pool_t = torch.from_numpy(img).cuda()
+    scores = torch.tensor([[0.5, 0.5]], dtype=torch.float32, device="cuda")
+    good = np.array([[0x80000000 | 1, 0x80000000 | 2]], dtype=np.int64)
+    bad = np.array([[0x80000000 | 1, 0x80000000 | 1000]], dtype=np.int64)
+    ex = _executor(2)
+    ex.execute(x, torch.from_numpy(good).cuda(), dev_records, scores=scores, slab_pack=pool_t)
+    assert _lib.check_device_errors() == 0
+    half = ex.execute(x, torch.from_numpy(bad).cuda(), dev_records, scores=scores, slab_pack=pool_t)
+    with pytest.raises(ValueError, match="route word"):
+        _lib.check_device_errors()
+    # the bad slot contributed nothing: equal to a single-slot route scaled by 0.5
+    one = ex.execute(x, torch.from_numpy(good[:, :1].repeat(2, axis=1)).cuda(), dev_records,
+                     scores=torch.tensor([[0.5, 0.0]], device="cuda"), slab_pack=pool_t)
+    assert torch.equal(half.view(torch.int16), one.view(torch.int16))
+    assert _lib.check_device_errors() == 0
+
+
 def test_f32_activations_decode(torch_mod, records, dev_records):
     torch = torch_mod
     say("case: decode f32 activations")
