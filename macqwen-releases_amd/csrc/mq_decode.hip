@@ -37,7 +37,6 @@ constexpr int kWaves = 4;  // waves per block
 constexpr int kThreads = 64 * kWaves;
 constexpr uint32_t kMaxSlots = 16;      // routed slots per token in the fused kernels
 constexpr uint32_t kMaxLayerTokens = 8;  // tokens of the fused routed layer
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ slices
 template <int SW>
@@ -52,11 +51,6 @@ struct Slice {
     else return wave_sum(v);
   }
 };
-
-__device__ __forceinline__ uint4 ld_nt(const uint32_t *p) {
-  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
 
 // (128+q_k, 128+q_{k+4}) bf16 pair from nibbles k and k+4 of w (one v_bfi_b32).
 __device__ __forceinline__ uint32_t nib_pair_bfi(uint32_t w, int k) {
@@ -105,10 +99,10 @@ struct XLane<BF16T> {
   XChunk part[1];
   float bias_sum;  // sum of the inputs, multiplies the group bias
   uint4 raw[4];
-  __device__ __forceinline__ void issue(const uint16_t *src, bool valid) {
-    const uint4 *v = reinterpret_cast<const uint4 *>(src);
+  // Loads the 64-byte chunk at byte offset `off` of the row (zeros when out of range).
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t row, uint32_t off) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) raw[j] = valid ? v[j] : make_uint4(0u, 0u, 0u, 0u);
+    for (int j = 0; j < 4; ++j) raw[j] = buf_load16(row, off + 16u * j);
   }
   __device__ __forceinline__ void finish() {
 #pragma unroll
@@ -126,18 +120,18 @@ struct XLane<F32T> {
   static constexpr int kParts = 2;
   XChunk part[2];
   float bias_sum;
-  float4 raw[8];
-  __device__ __forceinline__ void issue(const float *src, bool valid) {
-    const float4 *v = reinterpret_cast<const float4 *>(src);
+  uint4 raw[8];
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t row, uint32_t off) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) raw[j] = valid ? v[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int j = 0; j < 8; ++j) raw[j] = buf_load16(row, off + 16u * j);
   }
   __device__ __forceinline__ void finish() {
     uint32_t hi[16], lo[16];
     float s = 0.0f;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float f[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+      const float f[4] = {__uint_as_float(raw[j].x), __uint_as_float(raw[j].y), __uint_as_float(raw[j].z),
+                          __uint_as_float(raw[j].w)};
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int idx = 4 * j + k;
@@ -164,13 +158,21 @@ struct XLane<F32T> {
   }
 };
 
+// Row descriptor of an activation row of `in_w` values.
+template <class TT>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t x_rsrc(const typename TT::storage *row, uint32_t in_w) {
+  return make_rsrc(row, in_w * static_cast<uint32_t>(sizeof(typename TT::storage)));
+}
+
 template <class TT, int SW, int CPL>
-__device__ __forceinline__ void issue_x(XLane<TT> *x, const typename TT::storage *src, uint32_t in_w, int li) {
+__device__ __forceinline__ void issue_x(XLane<TT> *x, __amdgpu_buffer_rsrc_t row, uint32_t in_w, int li,
+                                        bool valid = true) {
   const uint32_t chunks = in_w >> 5;
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const uint32_t c = static_cast<uint32_t>(j * SW + li);
-    x[j].issue(src + c * 32, c < chunks);
+    const uint32_t off = valid && c < chunks ? c * 32u * static_cast<uint32_t>(sizeof(typename TT::storage)) : kOutOfRange;
+    x[j].issue(row, off);
   }
 }
 
@@ -188,9 +190,11 @@ struct RowLoad {
   uint16_t b[CPL];
 };
 
-// Issue the loads of one lane's chunks of row `row` (masked chunks read as 0).
+// Issue the loads of one lane's chunks of row `row`.  Masked chunks (row out
+// of range, tail chunk, invalid record) use an out-of-range offset and read as
+// zero, so the loads are issued back to back with no branches.
 template <int SW, int CPL>
-__device__ __forceinline__ void load_row(RowLoad<CPL> &r, const ExpertPtrs &e, uint32_t row, uint32_t in_w,
+__device__ __forceinline__ void load_row(RowLoad<CPL> &r, const ExpertRsrc &e, uint32_t row, uint32_t in_w,
                                          uint32_t group, int li, bool row_ok) {
   const uint32_t chunks = in_w >> 5;
   const uint32_t words = in_w >> 3;
@@ -199,16 +203,12 @@ __device__ __forceinline__ void load_row(RowLoad<CPL> &r, const ExpertPtrs &e, u
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
     const uint32_t c = static_cast<uint32_t>(j * SW + li);
-    if (row_ok && c < chunks) {
-      r.w[j] = ld_nt(e.w + static_cast<uint64_t>(row) * words + c * 4);
-      const uint64_t gi = static_cast<uint64_t>(row) * groups + (c >> shift);
-      r.s[j] = e.s[gi];
-      r.b[j] = e.b[gi];
-    } else {
-      r.w[j] = make_uint4(0u, 0u, 0u, 0u);
-      r.s[j] = 0;
-      r.b[j] = 0;
-    }
+    const bool ok = row_ok && c < chunks;
+    const uint32_t off_w = ok ? (row * words + c * 4u) * 4u : kOutOfRange;
+    const uint32_t off_g = ok ? (row * groups + (c >> shift)) * 2u : kOutOfRange;
+    r.w[j] = buf_load16<kNonTemporal>(e.w, off_w);
+    r.s[j] = buf_load2(e.s, off_g);
+    r.b[j] = buf_load2(e.b, off_g);
   }
 }
 
@@ -275,25 +275,22 @@ __global__ __launch_bounds__(kThreads) void gather_qmv_kernel(
   const int li = Sl::li(lane);
   const int sub = Sl::sub(lane);
   const uint32_t tiles_per_pair = (out_w + kTileRows - 1) / kTileRows;
-  const uint32_t tile = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const uint32_t tile = blockIdx.x * kWaves + wave_id();
   if (tile >= pairs * tiles_per_pair) return;  // wave-uniform
   const uint32_t pair = tile / tiles_per_pair;
   const uint32_t row0 = (tile % tiles_per_pair) * kTileRows;
+  const uint32_t token = pair / slots;
+  XLane<TT> xl[CPL];
+  issue_x<TT, SW, CPL>(xl, x_rsrc<TT>(x + static_cast<uint64_t>(slot_input ? pair : token) * in_w, in_w), in_w, li);
   const uint32_t word = routes ? routes[pair] : 0u;
   const ExpertPtrs e = expert_ptrs(proj, word, out_w, in_w, group, dense_count);
-  if (!e.ok) {  // wave-uniform: the word belongs to the wave's pair
-    if (lane == 0) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
-    return;
-  }
-  const uint32_t token = pair / slots;
-  const S *src = x + static_cast<uint64_t>(slot_input ? pair : token) * in_w;
-  XLane<TT> xl[CPL];
-  issue_x<TT, SW, CPL>(xl, src, in_w, li);
+  if (!e.ok && lane == 0) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);  // its rows read as zero
+  const ExpertRsrc er = expert_rsrc(e, out_w, in_w, group);
   RowLoad<CPL> r[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const uint32_t row = row0 + i * Sl::kRows + sub;
-    load_row<SW, CPL>(r[i], e, row, in_w, group, li, row < out_w);
+    load_row<SW, CPL>(r[i], er, row, in_w, group, li, row < out_w);
   }
   finish_x<TT, CPL>(xl);
 #pragma unroll
@@ -337,7 +334,7 @@ __global__ __launch_bounds__(kThreads) void gateup_kernel(
   constexpr int kTileRows = R * Sl::kRows;
   __shared__ RouteLds lds;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const uint32_t wave = wave_id();
   const int li = Sl::li(lane);
   const int sub = Sl::sub(lane);
   const uint32_t tiles_per_pair = (inter + kTileRows - 1) / kTileRows;
@@ -346,6 +343,18 @@ __global__ __launch_bounds__(kThreads) void gateup_kernel(
   const uint32_t total_tiles = min((routed_pairs + shared_pairs) * tiles_per_pair, tile_limit);
   const uint32_t shared_tiles = shared_pairs * tiles_per_pair;
   const uint32_t block_first = blockIdx.x * kWaves;
+
+  // The wave's tile: shared tiles first, then routed tiles.  The token (and
+  // so the activation row) is known before routing, so its loads go first.
+  const uint32_t tile = block_first + wave;
+  const bool tile_ok = tile < total_tiles;
+  const bool is_shared = tile < shared_tiles;
+  const uint32_t local = is_shared ? tile : tile - shared_tiles;
+  const uint32_t pair = is_shared ? routed_pairs + local / tiles_per_pair : local / tiles_per_pair;
+  const uint32_t row0 = (local % tiles_per_pair) * kTileRows;
+  const uint32_t token = min(is_shared ? pair - routed_pairs : pair / slots, tokens - 1u);
+  XLane<TT> xl[CPL];
+  issue_x<TT, SW, CPL>(xl, x_rsrc<TT>(x + static_cast<uint64_t>(token) * hidden, hidden), hidden, li, tile_ok);
 
   if constexpr (SELECT) {
     // Does this block own any routed tile?  (uniform per block)
@@ -373,20 +382,13 @@ __global__ __launch_bounds__(kThreads) void gateup_kernel(
     }
   }
 
-  const uint32_t tile = block_first + wave;
-  if (tile >= total_tiles) return;
-  // Shared tiles first, then routed tiles.
-  const bool is_shared = tile < shared_tiles;
-  const uint32_t local = is_shared ? tile : tile - shared_tiles;
-  const uint32_t pair = is_shared ? routed_pairs + local / tiles_per_pair : local / tiles_per_pair;
-  const uint32_t row0 = (local % tiles_per_pair) * kTileRows;
-  const uint32_t token = is_shared ? pair - routed_pairs : pair / slots;
+  if (!tile_ok) return;
   uint32_t word = 0u;
   if (!is_shared) {
     int32_t keep_t;
     if constexpr (SELECT) {
-      word = lds.word[pair];
-      keep_t = lds.keep[token];
+      word = uniform(lds.word[pair]);
+      keep_t = static_cast<int32_t>(uniform(static_cast<uint32_t>(lds.keep[token])));
     } else {
       word = routes[pair];
       keep_t = keeps != nullptr ? keeps[token] : static_cast<int32_t>(slots);
@@ -403,18 +405,15 @@ __global__ __launch_bounds__(kThreads) void gateup_kernel(
     eg = expert_ptrs(gate, word, inter, hidden, group, dense_count);
     eu = expert_ptrs(up, word, inter, hidden, group, dense_count);
   }
-  if (!eg.ok || !eu.ok) {
-    if (lane == 0) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
-    return;
-  }
-  XLane<TT> xl[CPL];
-  issue_x<TT, SW, CPL>(xl, x + static_cast<uint64_t>(token) * hidden, hidden, li);
+  if ((!eg.ok || !eu.ok) && lane == 0) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);  // rows read as zero
+  const ExpertRsrc rgs = expert_rsrc(eg, inter, hidden, group);
+  const ExpertRsrc rus = expert_rsrc(eu, inter, hidden, group);
   RowLoad<CPL> rg[R], ru[R];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const uint32_t row = row0 + i * Sl::kRows + sub;
-    load_row<SW, CPL>(rg[i], eg, row, hidden, group, li, row < inter);
-    load_row<SW, CPL>(ru[i], eu, row, hidden, group, li, row < inter);
+    load_row<SW, CPL>(rg[i], rgs, row, hidden, group, li, row < inter);
+    load_row<SW, CPL>(ru[i], rus, row, hidden, group, li, row < inter);
   }
   finish_x<TT, CPL>(xl);
   float gv[R], uv[R];
@@ -450,186 +449,107 @@ __global__ void swiglu_kernel(const typename TT::storage *__restrict__ g, const 
 
 enum SharedMode : int { kSharedNone = 0, kSharedY = 1, kSharedParts = 2, kSharedExpert = 3 };
 
-// Activation staging in LDS for the down kernel.  Each 32-input chunk of each
-// source row (routed slot or shared expert) is stored already converted to the
-// pair layout, plane-major so that consecutive lanes read consecutive 16-byte
-// words: plane q (q < 4*kParts) holds word q of every chunk, followed by
-// kParts chunk sums and the bias sum.
-template <class TT>
-struct StagedX {
-  static constexpr int kParts = XLane<TT>::kParts;
-  static constexpr uint32_t kBytesPerChunk = kParts * 64 + (kParts + 1) * 4;
-  uint4 *q;
-  float *sums;
-  uint32_t units;
-  __device__ __forceinline__ StagedX(unsigned char *smem, uint32_t n_units)
-      : q(reinterpret_cast<uint4 *>(smem)),
-        sums(reinterpret_cast<float *>(smem + static_cast<size_t>(n_units) * kParts * 64)),
-        units(n_units) {}
-  __device__ __forceinline__ void store(const XLane<TT> &x, uint32_t u) const {
-#pragma unroll
-    for (int p = 0; p < kParts; ++p) {
-#pragma unroll
-      for (int w = 0; w < 4; ++w)
-        q[(p * 4 + w) * units + u] = make_uint4(x.part[p].p[4 * w], x.part[p].p[4 * w + 1], x.part[p].p[4 * w + 2],
-                                                x.part[p].p[4 * w + 3]);
-      sums[p * units + u] = x.part[p].osum;
-    }
-    sums[kParts * units + u] = x.bias_sum;
-  }
-  __device__ __forceinline__ void load(XLane<TT> &x, uint32_t u) const {
-#pragma unroll
-    for (int p = 0; p < kParts; ++p) {
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint4 v = q[(p * 4 + w) * units + u];
-        x.part[p].p[4 * w] = v.x;
-        x.part[p].p[4 * w + 1] = v.y;
-        x.part[p].p[4 * w + 2] = v.z;
-        x.part[p].p[4 * w + 3] = v.w;
-      }
-      x.part[p].osum = sums[p * units + u];
-    }
-    x.bias_sum = sums[kParts * units + u];
-  }
-};
-
-// Down + score combine + shared epilogue for one token and Slice<SW>::kRows
-// output rows per wave.  For each routed slot s < keep: d = T(W_down .
-// act[t,s]); acc += float(d) * float(score[t,s]) in float32 with no
-// contraction, in slot order (models/flashnext/metal_runtime.py:291-336).
-//
-// Order of work: route words, scores and the first activation chunk of each
-// thread are loaded first; then every slot's weight rows are issued (NS slots
-// including the shared expert, inactive ones masked to zero); the activation
-// chunks are converted into LDS while the weights are in flight; finally all
-// NS row dots are computed without branches (independent chains) and
-// combined in slot order.
-template <class TT, int SW, int CPL, int NS>
+// Down + score combine + shared epilogue.  A block owns Slice<SW>::kRows
+// output rows of one token; its four waves split the token's active sources
+// (routed slots s < keep, then the shared expert) round-robin, so every wave
+// streams only its sources' weight rows and activation chunks, and the grid
+// has (hidden / kRows) * tokens blocks to spread the weight stream over the
+// whole chip.  Each wave handles its sources in batches of SPW: activations
+// issued first, then the weight rows, then the row dots (independent chains).
+// The T-rounded projections d go to LDS and wave 0 combines them in slot
+// order: acc += float(d) * float(score[t,s]) in float32 with no contraction
+// (models/flashnext/metal_runtime.py:291-336), then T(acc) and the shared
+// epilogue.  Padded slots (s >= keep) carry score 0 and are skipped.
+template <class TT, int SW, int CPL, int SPW>
 __global__ __launch_bounds__(kThreads) void down_combine_kernel(
     const typename TT::storage *__restrict__ act, MqProjection down, SharedExpert shared,
     const uint32_t *__restrict__ routes, const void *__restrict__ scores, int score_dtype,
     const int32_t *__restrict__ keeps, int shared_mode, const typename TT::storage *__restrict__ shared_vec,
     const uint16_t *__restrict__ shared_gate, typename TT::storage *__restrict__ out, uint32_t tokens,
-    uint32_t slots, uint32_t hidden, uint32_t inter, uint32_t group, uint32_t tiles_per_token,
-    uint32_t dense_count, unsigned int *__restrict__ err) {
+    uint32_t slots, uint32_t hidden, uint32_t inter, uint32_t group, uint32_t dense_count,
+    unsigned int *__restrict__ err) {
   using S = typename TT::storage;
   using Sl = Slice<SW>;
-  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr uint32_t kMaxSources = kMaxSlots + 1;
+  __shared__ float dsum[kMaxSources][Sl::kRows];
 
   const int lane = threadIdx.x & 63;
+  const uint32_t wave = wave_id();
   const int li = Sl::li(lane);
   const int sub = Sl::sub(lane);
   const uint32_t token = blockIdx.y;
-  const uint32_t tile = blockIdx.x * kWaves + (threadIdx.x >> 6);
-  const bool tile_ok = tile < tiles_per_token;
-  const uint32_t row = tile * Sl::kRows + sub;
-  const bool row_ok = tile_ok && row < hidden;
+  const uint32_t row = blockIdx.x * Sl::kRows + sub;
+  const bool row_ok = row < hidden;
   const uint32_t keep = keeps ? min(static_cast<uint32_t>(keeps[token]), slots) : slots;
   const bool with_shared_expert = shared_mode == kSharedExpert;
-  const uint32_t n_src = slots + (with_shared_expert ? 1u : 0u);
-  const uint32_t cps = inter >> 5;  // chunks per source row
-  const uint32_t units = n_src * cps;
-  const StagedX<TT> stage(smem, units);
-
-  // Small per-token inputs first.
-  uint32_t word[NS];
-  float score[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    word[s] = 0u;
-    score[s] = 0.0f;
-    if (static_cast<uint32_t>(s) < keep) {
-      const uint64_t pair = static_cast<uint64_t>(token) * slots + s;
-      word[s] = routes[pair];
-      score[s] = score_dtype == MQ_BF16 ? bf16_to_f32(static_cast<const uint16_t *>(scores)[pair])
-                                        : static_cast<const float *>(scores)[pair];
-    }
-  }
+  const uint32_t n_act = keep + (with_shared_expert ? 1u : 0u);
   const uint32_t routed_pairs = tokens * slots;
-  auto unit_source = [&](uint32_t u, bool &valid) -> const S * {
-    const uint32_t src = u / cps;
-    const uint32_t c = u % cps;
-    valid = u < units && (src >= slots || src < keep);
-    const uint64_t pair = src < slots ? static_cast<uint64_t>(token) * slots + src
-                                      : static_cast<uint64_t>(routed_pairs) + token;
-    return act + pair * inter + c * 32u;
-  };
-  XLane<TT> first;
-  bool first_ok;
-  const S *first_src = unit_source(threadIdx.x, first_ok);
-  first.issue(first_src, first_ok);
+  const uint64_t pair0 = static_cast<uint64_t>(token) * slots;
 
-  RowLoad<CPL> rows[NS];
-  bool slot_ok[NS];
+  // Small per-token inputs, all issued up front (no load waits on another).
+  float score[kMaxSlots];
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const uint32_t su = static_cast<uint32_t>(s);
-    const bool routed = su < keep;
-    const bool is_shared = with_shared_expert && su == slots;
-    ExpertPtrs e{nullptr, nullptr, nullptr, false};
-    if (routed) e = expert_ptrs(down, word[s], hidden, inter, group, dense_count);
-    else if (is_shared) e = expert_ptrs(shared.p[2], 0u, hidden, inter, group, 1u);
-    slot_ok[s] = e.ok;
-    if ((routed || is_shared) && !e.ok && lane == 0 && tile_ok) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
-    load_row<SW, CPL>(rows[s], e, row, inter, group, li, row_ok && e.ok);
+  for (uint32_t s = 0; s < kMaxSlots; ++s) {
+    const uint64_t pair = pair0 + min(s, slots - 1u);
+    score[s] = score_dtype == MQ_BF16 ? bf16_to_f32(static_cast<const uint16_t *>(scores)[pair])
+                                      : static_cast<const float *>(scores)[pair];
   }
+  float shared_in = 0.0f, gate_in = 0.0f;
+  if (shared_mode == kSharedY || shared_mode == kSharedParts)
+    shared_in = TT::load(shared_vec[static_cast<uint64_t>(token) * hidden + min(row, hidden - 1u)]);
+  if (shared_mode == kSharedParts || with_shared_expert) gate_in = bf16_to_f32(shared_gate[token]);
 
-  first.finish();
-  if (first_ok) stage.store(first, threadIdx.x);
-  for (uint32_t u = threadIdx.x + kThreads; u < units; u += kThreads) {
-    bool ok;
-    const S *src = unit_source(u, ok);
-    if (ok) {
-      XLane<TT> x;
-      x.issue(src, true);
-      x.finish();
-      stage.store(x, u);
+  for (uint32_t base = wave; base < n_act; base += kWaves * SPW) {
+    XLane<TT> xl[SPW][CPL];
+    RowLoad<CPL> rw[SPW];
+    uint32_t word[SPW];
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {  // route words and activations first
+      const uint32_t a = base + kWaves * i;
+      word[i] = routes[pair0 + min(a, slots - 1u)];
+      const uint64_t pair = a < keep ? pair0 + a : static_cast<uint64_t>(routed_pairs) + token;
+      issue_x<TT, SW, CPL>(xl[i], x_rsrc<TT>(act + pair * inter, inter), inter, li, a < n_act);
+    }
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {  // then the weight rows
+      const uint32_t a = base + kWaves * i;
+      ExpertPtrs e{nullptr, nullptr, nullptr, false};
+      if (a < keep) e = expert_ptrs(down, word[i], hidden, inter, group, dense_count);
+      else if (a < n_act) e = expert_ptrs(shared.p[2], 0u, hidden, inter, group, 1u);
+      if (a < n_act && !e.ok && lane == 0) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
+      load_row<SW, CPL>(rw[i], expert_rsrc(e, hidden, inter, group), row, inter, group, li, row_ok);
+    }
+    float v[SPW];
+#pragma unroll
+    for (int i = 0; i < SPW; ++i) {
+      finish_x<TT, CPL>(xl[i]);
+      v[i] = Sl::reduce(row_partial<TT, CPL>(rw[i], xl[i]));
+    }
+    if (li == 0) {
+#pragma unroll
+      for (int i = 0; i < SPW; ++i) {
+        const uint32_t a = base + kWaves * i;
+        if (a < n_act) dsum[a][sub] = TT::round(v[i]);  // a bad route reads as zero weights: d = 0
+      }
     }
   }
   __syncthreads();
-  if (!tile_ok) return;
+  if (wave != 0 || li != 0 || !row_ok) return;
 
-  float v[NS];
-#pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    // Inactive slots have all-zero weight rows and read slot 0's activations,
-    // so they add nothing; computing them keeps the loop free of branches.
-    const uint32_t su = static_cast<uint32_t>(s);
-    const bool active = su < keep || (with_shared_expert && su == slots);
-    const uint32_t src = active ? su : 0u;
-    XLane<TT> xl[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const uint32_t c = min(static_cast<uint32_t>(j * SW + li), cps - 1u);
-      stage.load(xl[j], src * cps + c);
-    }
-    v[s] = Sl::reduce(row_partial<TT, CPL>(rows[s], xl));
-  }
-
-  // Padded slots (s >= keep) carry score 0 and would add exact zeros: skipped.
   float acc = 0.0f;
-  float shared_v = 0.0f;
 #pragma unroll
-  for (int s = 0; s < NS; ++s) {
-    const uint32_t su = static_cast<uint32_t>(s);
-    if (su < keep && slot_ok[s]) acc = __fadd_rn(acc, __fmul_rn(TT::round(v[s]), score[s]));
-    if (with_shared_expert && su == slots) shared_v = v[s];
+  for (uint32_t s = 0; s < kMaxSlots; ++s)
+    if (s < keep) acc = __fadd_rn(acc, __fmul_rn(dsum[s][sub], score[s]));
+  const float routed = TT::round(acc);
+  float final_value = routed;
+  if (shared_mode == kSharedY) {
+    final_value = __fadd_rn(routed, shared_in);
+  } else if (shared_mode == kSharedParts) {
+    final_value = __fadd_rn(routed, TT::round(__fmul_rn(shared_in, gate_in)));
+  } else if (with_shared_expert) {
+    final_value = __fadd_rn(routed, TT::round(__fmul_rn(dsum[keep][sub], gate_in)));
   }
-  if (li == 0 && row_ok) {
-    const uint64_t idx = static_cast<uint64_t>(token) * hidden + row;
-    const float routed = TT::round(acc);
-    float final_value = routed;
-    if (shared_mode == kSharedY) {
-      final_value = __fadd_rn(routed, TT::load(shared_vec[idx]));
-    } else if (shared_mode == kSharedParts) {
-      const float comp = TT::round(__fmul_rn(TT::load(shared_vec[idx]), bf16_to_f32(shared_gate[token])));
-      final_value = __fadd_rn(routed, comp);
-    } else if (with_shared_expert) {
-      final_value = __fadd_rn(routed, TT::round(__fmul_rn(TT::round(shared_v), bf16_to_f32(shared_gate[token]))));
-    }
-    out[idx] = TT::store(final_value);
-  }
+  out[static_cast<uint64_t>(token) * hidden + row] = TT::store(final_value);
 }
 
 // ------------------------------------------------------------------ dispatch
@@ -736,17 +656,16 @@ int launch_gateup(const MqMoeArgs &a, const SharedExpert &shared, bool has_share
   return check_launch("gateup_kernel");
 }
 
-template <class TT, int SW, int CPL, int NS>
-void launch_down_ns(const MqMoeArgs &a, const SharedExpert &shared, int shared_mode,
-                    const typename TT::storage *shared_vec, const int32_t *keeps, const typename TT::storage *act,
-                    unsigned int *err, size_t lds, hipStream_t stream) {
+template <class TT, int SW, int CPL, int SPW>
+void launch_down_spw(const MqMoeArgs &a, const SharedExpert &shared, int shared_mode,
+                     const typename TT::storage *shared_vec, const int32_t *keeps, const typename TT::storage *act,
+                     unsigned int *err, hipStream_t stream) {
   using S = typename TT::storage;
-  const uint32_t tiles_per_token = ceil_div(a.hidden, Slice<SW>::kRows);
-  const dim3 grid(ceil_div(tiles_per_token, kWaves), a.tokens);
-  hipLaunchKernelGGL((down_combine_kernel<TT, SW, CPL, NS>), grid, dim3(kThreads), lds, stream, act, a.down, shared,
+  const dim3 grid(ceil_div(a.hidden, Slice<SW>::kRows), a.tokens);
+  hipLaunchKernelGGL((down_combine_kernel<TT, SW, CPL, SPW>), grid, dim3(kThreads), 0, stream, act, a.down, shared,
                      a.routes, a.scores, a.score_dtype, keeps, shared_mode, shared_vec, a.shared_gate,
-                     static_cast<S *>(a.out), a.tokens, a.slots, a.hidden, a.inter, a.group_size, tiles_per_token,
-                     a.expert_count, err);
+                     static_cast<S *>(a.out), a.tokens, a.slots, a.hidden, a.inter, a.group_size, a.expert_count,
+                     err);
 }
 
 template <class TT>
@@ -754,13 +673,20 @@ int launch_down(const MqMoeArgs &a, const SharedExpert &shared, int shared_mode,
                 const int32_t *keeps, const typename TT::storage *act, unsigned int *err, hipStream_t stream) {
   const Geometry g = geometry(a.inter);
   const uint32_t n_src = a.slots + (shared_mode == kSharedExpert ? 1u : 0u);
-  const size_t lds = static_cast<size_t>(n_src) * (a.inter / 32) * StagedX<TT>::kBytesPerChunk;
-  if (lds > 64 * 1024) return fail(MQ_ERR_UNSUPPORTED, "activation staging needs %zu bytes of LDS", lds);
+  const uint32_t per_wave = ceil_div(n_src, kWaves);
   MQ_GEOM_SWITCH(g, {
-    if (n_src <= 4) launch_down_ns<TT, SW, CPL, 4>(a, shared, shared_mode, shared_vec, keeps, act, err, lds, stream);
-    else if (n_src <= 8) launch_down_ns<TT, SW, CPL, 8>(a, shared, shared_mode, shared_vec, keeps, act, err, lds, stream);
-    else if (n_src <= 12) launch_down_ns<TT, SW, CPL, 12>(a, shared, shared_mode, shared_vec, keeps, act, err, lds, stream);
-    else launch_down_ns<TT, SW, CPL, 17>(a, shared, shared_mode, shared_vec, keeps, act, err, lds, stream);
+    // Sources per batch: all of a wave's sources when their registers fit.
+    if constexpr (CPL == 1) {
+      if (per_wave <= 1) launch_down_spw<TT, SW, CPL, 1>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+      else if (per_wave <= 2) launch_down_spw<TT, SW, CPL, 2>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+      else if (per_wave <= 3) launch_down_spw<TT, SW, CPL, 3>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+      else launch_down_spw<TT, SW, CPL, 5>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+    } else if constexpr (CPL == 2) {
+      if (per_wave <= 1) launch_down_spw<TT, SW, CPL, 1>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+      else launch_down_spw<TT, SW, CPL, 2>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+    } else {
+      launch_down_spw<TT, SW, CPL, 1>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+    }
   });
   return check_launch("down_combine_kernel");
 }

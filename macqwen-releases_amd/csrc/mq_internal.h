@@ -244,6 +244,55 @@ __device__ __forceinline__ ExpertPtrs expert_ptrs(const MqProjection &p, uint32_
   return r;
 }
 
+// ---------------------------------------------------------------- buffer resources
+// Raw buffer descriptors (gfx9 descriptor word 3).  A buffer load whose byte
+// offset lies beyond the descriptor's size returns zero without touching
+// memory, so tails, masked rows and invalid records are handled without any
+// branch around a load (a branch would make the compiler wait for each load
+// before the next is issued).
+constexpr int kBufferWord3 = 0x00020000;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // byte offset beyond every descriptor used here
+constexpr int kNonTemporal = 2;                // buffer-load cache policy: non-temporal (streamed once)
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           kBufferWord3);
+}
+
+template <int AUX = 0>
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, AUX);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, 0);
+}
+
+// Descriptors of one projection of one expert (size 0 when the word is invalid).
+struct ExpertRsrc {
+  __amdgpu_buffer_rsrc_t w, s, b;
+};
+
+__device__ __forceinline__ ExpertRsrc expert_rsrc(const ExpertPtrs &e, uint32_t out_w, uint32_t in_w,
+                                                  uint32_t group) {
+  const uint32_t wbytes = e.ok ? out_w * (in_w / 8u) * 4u : 0u;
+  const uint32_t gbytes = e.ok ? out_w * (in_w / group) * 2u : 0u;
+  return {make_rsrc(e.w, wbytes), make_rsrc(e.s, gbytes), make_rsrc(e.b, gbytes)};
+}
+
+// Wave index as a scalar (uniform) value, so that everything derived from it
+// (tiles, pairs, route words, record addresses) stays in scalar registers.
+__device__ __forceinline__ uint32_t wave_id() {
+  return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6)));
+}
+
+__device__ __forceinline__ uint32_t uniform(uint32_t v) {
+  return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(v)));
+}
+
 // Raise a device error flag (vector atomic from one lane).
 __device__ __forceinline__ void raise_flag(unsigned int *flags, unsigned int bit) {
   if (flags != nullptr)

@@ -1,5 +1,6 @@
-// Router selection for one token by one wave: softmax (float64) over bf16
-// logits, top-k on the bf16 gate bits (gate descending, expert ascending),
+// Router selection for one token by one wave: softmax over bf16 logits
+// (float32 with an exactness guard, float64 fallback), top-k on the bf16 gate
+// bits (gate descending, expert ascending),
 // adaptive keep and padding, bf16 renorm and slot words.
 //
 // Restates the chain of models/flashnext/compiled.py:61-71 and
@@ -7,8 +8,8 @@
 // argpartition top-k, take_along_axis, topk_mass, _keep_for_mass, padding of
 // dropped slots with slot 0's expert and score 0, and
 // scores / (mass + blend * (selected - mass)) in bf16 arithmetic.  Logits are
-// exact-rounded bf16 and the softmax is evaluated in float64, so the bf16
-// gates (and everything after) are reproducible bit for bit.
+// exact-rounded bf16 and every bf16 gate equals the correctly rounded softmax
+// value, so the gates (and everything after) are reproducible bit for bit.
 #pragma once
 
 #include <math.h>
@@ -76,21 +77,19 @@ struct SelectLane {
 };
 
 // Top-k over unique keys: k rounds of "wave max of the lanes' best key".
-__device__ __forceinline__ void select_keys(uint32_t *key, uint32_t k, uint32_t *sel) {
+// Lane j keeps the j-th selected key (descending); other lanes get 0.
+__device__ __forceinline__ uint32_t select_keys(uint32_t *key, uint32_t k, int lane) {
+  uint32_t mine = 0u;
+  for (uint32_t j = 0; j < k; ++j) {
+    uint32_t best = 0u;
 #pragma unroll
-  for (uint32_t j = 0; j < kSelMaxTopK; ++j) {
-    sel[j] = 0u;
-    if (j < k) {
-      uint32_t best = 0u;
+    for (int i = 0; i < kSelMaxPerLane; ++i) best = key[i] > best ? key[i] : best;
+    best = wave_max_u32_uniform(best);
+    mine = static_cast<uint32_t>(lane) == j ? best : mine;
 #pragma unroll
-      for (int i = 0; i < kSelMaxPerLane; ++i) best = key[i] > best ? key[i] : best;
-      best = wave_max_u32_uniform(best);
-      sel[j] = best;
-#pragma unroll
-      for (int i = 0; i < kSelMaxPerLane; ++i)
-        if (key[i] == best) key[i] = 0u;
-    }
+    for (int i = 0; i < kSelMaxPerLane; ++i) key[i] = key[i] == best ? 0u : key[i];
   }
+  return mine;
 }
 
 __device__ __forceinline__ float wave_max_f32_uniform(float v) {
@@ -105,24 +104,49 @@ __device__ __forceinline__ float wave_max_f32_uniform(float v) {
   return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
+__device__ __forceinline__ float readlane_f(float v, uint32_t lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), static_cast<int>(lane)));
+}
+
+// Selection window: float32 gates whose low 16 bits lie within this many
+// float32 ulps of the bf16 rounding midpoint (0x8000) may round differently
+// from the exact gate (see select_token).
+constexpr int kMidpointWindow = 64;
+// log2(e) split into float32 head and tail: d * log2(e) = fma(d, hi, d * lo)
+// carries one rounding (|error| <= 2^-19 for |d| <= 32).
+constexpr float kLog2eHi = 1.44269502162933349609375f;
+constexpr float kLog2eLo = 1.925963033500011e-08f;
+
 // All 64 lanes of the wave must call this together.
 //
-// The gates are first evaluated in float32: exp(l - m) by expf (<= 2 ulp;
-// l - m is exact), a fixed-order sum and a correctly rounded division, which
-// bounds each gate's relative error by about 16 float32 ulps.  A gate's bf16
-// bits are then exact unless its float32 value lies within that bound of a
-// bf16 rounding midpoint.  Only gates within one bf16 step of the k-th gate
-// can change the selection or the scores; if any of them is that close to a
-// midpoint the token is re-evaluated in float64 (exp, sum and division),
-// which is exact for all practical inputs.
+// The gates are first evaluated in float32: e = exp2((l - m) * log2(e)) with
+// the hardware exp2 (l - m is exact for bf16 logits within 32 of the max; the
+// argument carries one rounding, <= 2^-19, i.e. <= 22 ulps of the result,
+// and exp2 itself about 1 ulp), a fixed-order tree sum of depth <= 14
+// (<= 14 ulps) and one correctly rounded reciprocal and product (1 ulp): each
+// gate is within ~40 float32 ulps of the exact value, inside kMidpointWindow.  A gate's bf16 bits are then exact unless its
+// float32 value lies within the window of a bf16 rounding midpoint (or its
+// logit is more than 32 below the max).  Only gates within one bf16 step of
+// the k-th gate can change the selection or the scores; if any of them is that
+// close to a midpoint the token is re-evaluated in float64 (exp, sum and
+// division), which is exact for all practical inputs.
 __device__ __forceinline__ SelectLane select_token(const SelectParams &a, uint32_t t, int lane) {
   const uint16_t *lrow = a.logits + static_cast<uint64_t>(t) * a.experts;
+  // All loads are unconditional (clamped indices, results masked afterwards)
+  // so they are issued back to back; the slot table is fetched alongside the
+  // logits and indexed later through a lane permute.
   float lv[kSelMaxPerLane];
+  uint32_t slot_of[kSelMaxPerLane];
+#pragma unroll
+  for (int i = 0; i < kSelMaxPerLane; ++i) {
+    const uint32_t e = min(static_cast<uint32_t>(lane + 64 * i), a.experts - 1u);
+    lv[i] = bf16_to_f32(lrow[e]);
+    slot_of[i] = a.slot_table ? a.slot_table[e] : 0u;
+  }
   float m = -INFINITY;
 #pragma unroll
   for (int i = 0; i < kSelMaxPerLane; ++i) {
-    const uint32_t e = lane + 64 * i;
-    lv[i] = e < a.experts ? bf16_to_f32(lrow[e]) : -INFINITY;
+    if (static_cast<uint32_t>(lane + 64 * i) >= a.experts) lv[i] = -INFINITY;
     m = fmaxf(m, lv[i]);
   }
   m = wave_max_f32_uniform(m);
@@ -131,13 +155,15 @@ __device__ __forceinline__ SelectLane select_token(const SelectParams &a, uint32
   float sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < kSelMaxPerLane; ++i) {
-    const uint32_t e = lane + 64 * i;
-    const float d = lv[i] - m;  // exact while |d| <= 32 for bf16 inputs of this range
+    const float d = lv[i] - m;
     wide[i] = !(d >= -32.0f);
-    ev[i] = e < a.experts ? expf(d) : 0.0f;
+    ev[i] = static_cast<uint32_t>(lane + 64 * i) < a.experts
+                ? __builtin_amdgcn_exp2f(__fmaf_rn(d, kLog2eHi, __fmul_rn(d, kLog2eLo)))
+                : 0.0f;
     sum += ev[i];
   }
   sum = wave_sum(sum);
+  const float rsum = __fdiv_rn(1.0f, sum);
   // Key: bf16 gate bits (non-negative, so they order like values) high,
   // inverted expert index low (ties -> lower index).  Keys are unique.
   uint32_t key[kSelMaxPerLane], gbits[kSelMaxPerLane];
@@ -145,19 +171,15 @@ __device__ __forceinline__ SelectLane select_token(const SelectParams &a, uint32
 #pragma unroll
   for (int i = 0; i < kSelMaxPerLane; ++i) {
     const uint32_t e = lane + 64 * i;
-    const float g = __fdiv_rn(ev[i], sum);
+    const float g = __fmul_rn(ev[i], rsum);
     const int low = static_cast<int>(__float_as_uint(g) & 0xffffu);
     gbits[i] = e < a.experts ? f32_to_bf16(g) : 0u;
-    near[i] = e < a.experts && (abs(low - 0x8000) <= 48 || wide[i]);
+    near[i] = e < a.experts && (abs(low - 0x8000) <= kMidpointWindow || wide[i]);
     key[i] = e < a.experts ? (gbits[i] << 16) | (0xffffu - e) : 0u;
   }
   const uint32_t k = a.top_k;
-  uint32_t sel[kSelMaxTopK];
-  select_keys(key, k, sel);
-  uint32_t kth = 0u;
-#pragma unroll
-  for (uint32_t j = 0; j < kSelMaxTopK; ++j)
-    if (j + 1 == k) kth = sel[j] >> 16;
+  uint32_t mine = select_keys(key, k, lane);
+  const uint32_t kth = readlane_u(mine, static_cast<int>(k - 1u)) >> 16;
   bool risky = false;
 #pragma unroll
   for (int i = 0; i < kSelMaxPerLane; ++i) risky |= near[i] && gbits[i] + 1u >= kth;
@@ -176,59 +198,53 @@ __device__ __forceinline__ SelectLane select_token(const SelectParams &a, uint32
       const uint32_t e = lane + 64 * i;
       key[i] = e < a.experts ? (static_cast<uint32_t>(f64_to_bf16(dv[i] / dsum)) << 16) | (0xffffu - e) : 0u;
     }
-    select_keys(key, k, sel);
+    mine = select_keys(key, k, lane);
   }
-  uint32_t ind[kSelMaxTopK];
-  float raw[kSelMaxTopK];
+  // Lane j < k: slot j.  Reductions over slots run in slot order (readlane).
+  const bool slot_lane = static_cast<uint32_t>(lane) < k;
+  uint32_t ind = 0xffffu - (mine & 0xffffu);
+  const float raw = slot_lane ? bf16_to_f32(static_cast<uint16_t>(mine >> 16)) : 0.0f;
   float mass32 = 0.0f;
-#pragma unroll
-  for (uint32_t j = 0; j < kSelMaxTopK; ++j) {
-    ind[j] = 0xffffu - (sel[j] & 0xffffu);
-    raw[j] = bf16_to_f32(static_cast<uint16_t>(sel[j] >> 16));
-    if (j < k) mass32 = __fadd_rn(mass32, raw[j]);
-  }
+  for (uint32_t j = 0; j < k; ++j) mass32 = __fadd_rn(mass32, readlane_f(raw, j));
   const float mass = round_bf16(mass32);
   uint32_t keep = k;
   if (a.threshold < 1.0f) {
     double total = 0.0;
-#pragma unroll
-    for (uint32_t j = 0; j < kSelMaxTopK; ++j)
-      if (j < k) total += static_cast<double>(raw[j]);
+    for (uint32_t j = 0; j < k; ++j) total += static_cast<double>(readlane_f(raw, j));
     double accumulated = 0.0;
     uint32_t found = k;
-#pragma unroll
-    for (uint32_t j = 0; j < kSelMaxTopK; ++j) {
-      if (j < k && found == k) {
-        accumulated += static_cast<double>(raw[j]) / total;
-        if (accumulated >= static_cast<double>(a.threshold)) found = j + 1;
+    for (uint32_t j = 0; j < k; ++j) {
+      accumulated += static_cast<double>(readlane_f(raw, j)) / total;
+      if (accumulated >= static_cast<double>(a.threshold)) {
+        found = j + 1;
+        break;
       }
     }
     const uint32_t minimum = a.min_keep < 1u ? 1u : (a.min_keep > k ? k : a.min_keep);
     keep = found > minimum ? found : minimum;
   }
-  float padded[kSelMaxTopK];
+  // Dropped slots repeat slot 0's expert with score 0.
+  const uint32_t ind0 = readlane_u(ind, 0);
+  const bool kept = static_cast<uint32_t>(lane) < keep;
+  ind = kept ? ind : ind0;
+  const float padded = kept ? raw : 0.0f;
   float sel32 = 0.0f;
-#pragma unroll
-  for (uint32_t j = 0; j < kSelMaxTopK; ++j) {
-    if (j >= keep) ind[j] = ind[0];
-    padded[j] = j < keep ? raw[j] : 0.0f;
-    if (j < k) sel32 = __fadd_rn(sel32, padded[j]);
-  }
+  for (uint32_t j = 0; j < k; ++j) sel32 = __fadd_rn(sel32, readlane_f(padded, j));
   const float selected = round_bf16(sel32);
   const float blend = round_bf16(a.blend);
   const float norm = badd(mass, bmul(blend, bsub(selected, mass)));
-  SelectLane out{0u, 0u, 0.0f, 0.0f, keep};
+  // slot_table[ind]: entry ind sits in register ind / 64 of lane ind % 64.
+  uint32_t slot = 0u;
 #pragma unroll
-  for (uint32_t j = 0; j < kSelMaxTopK; ++j) {
-    if (static_cast<uint32_t>(lane) == j) {
-      out.ind = ind[j];
-      out.raw = raw[j];
-      out.score = padded[j];
-    }
+  for (int i = 0; i < kSelMaxPerLane; ++i) {
+    const uint32_t v = static_cast<uint32_t>(
+        __builtin_amdgcn_ds_bpermute(static_cast<int>((ind & 63u) << 2), static_cast<int>(slot_of[i])));
+    slot = (ind >> 6) == static_cast<uint32_t>(i) ? v : slot;
   }
-  if (static_cast<uint32_t>(lane) < k) {
-    out.score = bdiv(out.score, norm);
-    out.word = a.slot_table ? (MQ_SLOT_BIT | a.slot_table[out.ind]) : out.ind;
+  SelectLane out{ind, 0u, raw, 0.0f, keep};
+  if (slot_lane) {
+    out.score = bdiv(padded, norm);
+    out.word = a.slot_table ? (MQ_SLOT_BIT | slot) : ind;
   }
   return out;
 }

@@ -146,6 +146,33 @@ def test_router_bit_exact(torch_mod, tokens):
     assert np.array_equal(from_dev_bf16(res.shared_gate), sg)
 
 
+@pytest.mark.parametrize("scale", [0.3, 1.5, 6.0, "coarse"])
+def test_router_bit_exact_many_tokens(torch_mod, scale):
+    """8192 tokens per logit scale: the float32 softmax with its midpoint guard
+    must give the float64-exact bf16 gates, selection and scores every time
+    (coarse logits produce many exactly tied gates)."""
+    torch = torch_mod
+    say(f"case: router 8192 tokens scale={scale}")
+    from flashnext_hip import router
+
+    tokens = 8192
+    rng = np.random.default_rng({0.3: 60, 1.5: 61, 6.0: 62, "coarse": 63}[scale])
+    if scale == "coarse":
+        raw = np.round(rng.normal(0, 1.0, (tokens, 512)) * 4.0) / 4.0
+    else:
+        raw = rng.normal(0, scale, (tokens, 512))
+    logits = bf16.f32_to_bf16(raw.astype(np.float32))
+    perm = rng.permutation(512).astype(np.uint32)
+    res = router.route(None, None, 10, logits=to_dev_bf16(logits),
+                       slot_table=torch.from_numpy(perm.view(np.int32)).cuda())
+    torch.cuda.synchronize()
+    ref = orouter.route(None, None, 10, logits_bits=logits, slot_table=perm)
+    assert np.array_equal(res.inds.cpu().numpy().astype(np.uint32), ref["inds"])
+    assert np.array_equal(from_dev_bf16(res.scores_raw), ref["scores_raw"])
+    assert np.array_equal(from_dev_bf16(res.scores), ref["scores"])
+    assert np.array_equal(res.routes.cpu().numpy().view(np.uint32), ref["routes"])
+
+
 def test_router_adaptive_keep_and_logits_input(torch_mod):
     torch = torch_mod
     say("case: router threshold=0.85 min_keep=2 from logits")
