@@ -141,20 +141,27 @@ typedef struct MqRouteArgs {
 
 /* Arguments of mq_moe_grouped: the >8-token (prefill / verify) path of
  * StreamingSwitchGLU._one_pass/_issue (models/flashnext/expert_cache.py:1743-1810):
- * gather_qmm gate/up -> SwiGLU -> gather_qmm down with token sorting, then
- * the bf16 generic combine (models/flashnext/adaptive_topk.py:274-277). */
+ * the (token, slot) rows are sorted by expert (build_plan, :750-760, and
+ * mlx-vlm _gather_sort), gather_qmm gate/up -> SwiGLU -> gather_qmm down run
+ * as grouped bf16 MFMA GEMMs over the sorted rows, the per-slot outputs are
+ * unsorted into y, and the bf16 generic combine
+ * (models/flashnext/adaptive_topk.py:274-277) produces out. */
 typedef struct MqGroupedArgs {
   const uint16_t *x;        /* [tokens, hidden] bf16 */
   MqProjection gate, up, down;
   const uint32_t *routes;   /* [tokens, slots] route words */
-  const uint16_t *scores;   /* [tokens, slots] bf16, or NULL (then only y is written) */
-  const uint16_t *shared;   /* optional [tokens, hidden] bf16 */
-  const uint16_t *shared_gate; /* optional [tokens] bf16 */
+  const uint16_t *scores;   /* [tokens, slots] bf16; required when out is set */
+  const uint16_t *shared;   /* optional precomputed shared expert output [tokens, hidden] bf16 */
+  const MqProjection *shared_expert; /* optional HOST array of 3 (gate, up, down) dense
+                                        single-expert projections, run as one more group */
+  const uint16_t *shared_gate; /* [tokens] bf16, required with shared or shared_expert */
   uint16_t *out;            /* [tokens, hidden] bf16 combined, or NULL */
-  uint16_t *y;              /* optional [tokens, slots, hidden] bf16 per-slot outputs */
+  uint16_t *y;              /* [tokens, slots, hidden] bf16 per-slot outputs (required) */
   void *workspace;          /* device scratch of mq_grouped_workspace_size() bytes */
   uint64_t workspace_bytes;
-  uint32_t tokens, slots, hidden, inter, expert_count, group_size;
+  uint32_t tokens, slots, hidden, inter;
+  uint32_t expert_count;    /* dense experts addressed by plain route ids (0 with a pool) */
+  uint32_t group_size;
 } MqGroupedArgs;
 
 /* ---- capability and errors (tests/bench/metal_runtime_native.mm:196-205) ---- */
@@ -235,8 +242,11 @@ int mq_moe_decode(const MqMoeArgs *args, void *stream);
 int mq_moe_layer(const MqRouteArgs *route, const MqMoeArgs *moe, void *stream);
 
 /* ---- prefill / verify grouped path ---- */
+/* Workspace bytes for mq_moe_grouped: `route_keys` is the number of distinct
+ * route targets (pool slots + plain expert ids addressable by the routes),
+ * `shared` is 1 when a shared expert runs as an extra group. */
 uint64_t mq_grouped_workspace_size(uint32_t tokens, uint32_t slots, uint32_t hidden,
-                                   uint32_t inter, uint32_t expert_count);
+                                   uint32_t inter, uint32_t route_keys, int shared);
 int mq_moe_grouped(const MqGroupedArgs *args, void *stream);
 
 /* ---- expert slot pool refill (models/flashnext/expert_pool.py:112-145) ----

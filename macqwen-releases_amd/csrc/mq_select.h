@@ -60,6 +60,13 @@ __device__ __forceinline__ float sigmoid_bf16(float g) {
   return g < 0.0f ? s : om;
 }
 
+// bf16 SwiGLU of bf16-valued g and u: bf16(bf16(g * sigmoid_bf16(g)) * u)
+// (models/flashnext/metal_runtime.py:278-287).
+__device__ __forceinline__ float swiglu_bf16(float g, float u) {
+  const float silu = round_bf16(__fmul_rn(g, sigmoid_bf16(g)));
+  return round_bf16(__fmul_rn(silu, u));
+}
+
 struct SelectParams {
   const uint16_t *logits;      // [tokens, experts] bf16
   const uint32_t *slot_table;  // [experts] or nullptr

@@ -129,6 +129,7 @@ class MqGroupedArgs(ctypes.Structure):
         ("routes", ctypes.c_void_p),
         ("scores", ctypes.c_void_p),
         ("shared", ctypes.c_void_p),
+        ("shared_expert", ctypes.c_void_p),  # host array of 3 MqProjection
         ("shared_gate", ctypes.c_void_p),
         ("out", ctypes.c_void_p),
         ("y", ctypes.c_void_p),
@@ -165,7 +166,7 @@ def _declare(lib) -> None:
         "mq_route_topk": ([c.POINTER(MqRouteArgs), vp], i32),
         "mq_moe_decode": ([c.POINTER(MqMoeArgs), vp], i32),
         "mq_moe_layer": ([c.POINTER(MqRouteArgs), c.POINTER(MqMoeArgs), vp], i32),
-        "mq_grouped_workspace_size": ([u32, u32, u32, u32, u32], u64),
+        "mq_grouped_workspace_size": ([u32, u32, u32, u32, u32, i32], u64),
         "mq_moe_grouped": ([c.POINTER(MqGroupedArgs), vp], i32),
         "mq_pool_refill_async": ([vp, u64, u64, vp, vp, u32, u64, vp, vp], i32),
     }

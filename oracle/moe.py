@@ -176,16 +176,17 @@ class ExpertRecordSet:
         self.shared = shared  # (gate_bank, up_bank, down_bank) with one expert, or None
 
 
-def expert_mlp(x_f32, banks, expert: int, dtype: str = "bf16"):
+def expert_mlp(x_f32, banks, expert: int, dtype: str = "bf16", weights: str = "exact"):
     """One expert: T(gate), T(up), swiglu, T(down) for rows ``x_f32`` ``[n, H]``.
 
-    Returns (gate, up, act, down) in T storage.
+    ``weights``: "exact" dequantized weights, or "bf16" tiles (see
+    ``ExpertBank.project``).  Returns (gate, up, act, down) in T storage.
     """
     gate_bank, up_bank, down_bank = banks
-    g = round_t_f64(gate_bank.project(x_f32, expert), dtype)
-    u = round_t_f64(up_bank.project(x_f32, expert), dtype)
+    g = round_t_f64(gate_bank.project(x_f32, expert, weights), dtype)
+    u = round_t_f64(up_bank.project(x_f32, expert, weights), dtype)
     a = swiglu(g, u, dtype)
-    d = round_t_f64(down_bank.project(to_f32(a, dtype), expert), dtype)
+    d = round_t_f64(down_bank.project(to_f32(a, dtype), expert, weights), dtype)
     return g, u, a, d
 
 
@@ -235,7 +236,7 @@ def decode_layer(x, routes_experts, scores, records: ExpertRecordSet, *,
 
 
 def prefill_layer(x_bits, inds, scores_bits, records: ExpertRecordSet, *,
-                  shared_gate_weight=None):
+                  shared_gate_weight=None, weights: str = "exact"):
     """Grouped (gather_qmm) path: per (token, slot) row the expert MLP in bf16,
     then the generic bf16 combine (``expert_cache.py:1790-1810``,
     ``adaptive_topk.py:274-277``).  Returns bf16 ``[T, H]`` and the per-slot
@@ -251,10 +252,10 @@ def prefill_layer(x_bits, inds, scores_bits, records: ExpertRecordSet, *,
     for e in np.unique(flat):
         rows = np.nonzero(flat == e)[0]
         t_idx, s_idx = rows // slots, rows % slots
-        _g, _u, _a, d = expert_mlp(xf[t_idx], (records.gate, records.up, records.down), int(e), "bf16")
+        _g, _u, _a, d = expert_mlp(xf[t_idx], (records.gate, records.up, records.down), int(e), "bf16", weights)
         y[t_idx, s_idx] = d
     if records.shared is not None and shared_gate_weight is not None:
-        _g, _u, _a, sd = expert_mlp(xf, records.shared, 0, "bf16")
+        _g, _u, _a, sd = expert_mlp(xf, records.shared, 0, "bf16", weights)
         sg = shared_gate_value(x_bits, shared_gate_weight)
         return generic_combine(y, scores_bits, sg, sd), y
     return generic_combine(y, scores_bits), y

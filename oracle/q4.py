@@ -146,9 +146,28 @@ class ExpertBank:
             self._dense[int(expert)] = cached
         return cached
 
-    def project(self, x_f, expert: int) -> np.ndarray:
-        """float64 ``x @ W_e.T`` for rows ``x_f`` ``[n, I]``."""
-        return np.asarray(x_f, dtype=np.float64) @ self.dense(expert).T
+    def dense_bf16(self, expert: int) -> np.ndarray:
+        """Weights as bf16 MFMA tiles hold them: bf16(fma_f32(q, s, b)), as float64."""
+        key = ("bf16", int(expert))
+        cached = self._dense.get(key)
+        if cached is None:
+            q = unpack_q4(self.packed[expert]).astype(np.float64)
+            s = np.repeat(bf16_to_f32(self.scales[expert]).astype(np.float64), self.group_size, axis=-1)
+            b = np.repeat(bf16_to_f32(self.biases[expert]).astype(np.float64), self.group_size, axis=-1)
+            # q*s + b is exact in float64 (4-bit q, 8-bit s, b aligned); one
+            # rounding to float32 reproduces the fused multiply-add.
+            cached = bf16_to_f32(f32_to_bf16((q * s + b).astype(np.float32))).astype(np.float64)
+            self._dense[key] = cached
+        return cached
+
+    def project(self, x_f, expert: int, weights: str = "exact") -> np.ndarray:
+        """float64 ``x @ W_e.T`` for rows ``x_f`` ``[n, I]``.
+
+        ``weights="exact"`` uses the exact dequantized weights; ``"bf16"``
+        uses them rounded to bf16 first (the grouped GEMM's MFMA tiles).
+        """
+        w = self.dense(expert) if weights == "exact" else self.dense_bf16(expert)
+        return np.asarray(x_f, dtype=np.float64) @ w.T
 
 
 def gather_qmm(x_bits, bank: ExpertBank, rhs_indices) -> np.ndarray:

@@ -268,3 +268,21 @@ def test_lru_assign_reference_kat():
     assert lru.hits == kat["expected_hits"] and lru.misses == kat["expected_misses"]
     with pytest.raises(ValueError):
         pool.LruSlots(kat["too_small_slots"])
+
+
+def test_bf16_tile_weights_are_rounded_exact_weights():
+    """The bf16-tile weight mode equals bf16(float32(exact dequant)): q*s + b is
+    exact in float64, so one float32 rounding is the fused multiply-add."""
+    from oracle import q4
+    from oracle.bf16 import bf16_to_f32, f32_to_bf16
+
+    rng = np.random.default_rng(5)
+    w = rng.normal(0, 0.02, (2, 64, 128)).astype(np.float32)
+    packed, scales, biases = q4.quantize_affine(w, 32)
+    bank = q4.ExpertBank(packed, scales, biases, 32)
+    for e in range(2):
+        exact = bank.dense(e)
+        tiles = bank.dense_bf16(e)
+        assert np.array_equal(tiles, bf16_to_f32(f32_to_bf16(exact.astype(np.float32))).astype(np.float64))
+        # a bf16 tile differs from the exact weight by at most half a bf16 ulp
+        assert np.all(np.abs(tiles - exact) <= np.abs(exact) * 2.0 ** -8 + 1e-30)
