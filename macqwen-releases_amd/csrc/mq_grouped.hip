@@ -30,11 +30,12 @@
 namespace mq {
 namespace {
 
-constexpr uint32_t kTileRows = 128;  // sorted rows (tokens) per tile
-constexpr uint32_t kBK = 64;         // inputs per pipeline stage
-constexpr uint32_t kLdsK = kBK + 8;  // padded LDS row (bf16), keeps 16-byte reads conflict-free
-constexpr uint32_t kGateUpFeatures = 64;  // per gate/up block: 64 gate + 64 up weight rows
-constexpr uint32_t kDownFeatures = 128;   // per down block
+constexpr uint32_t kTileRows = 128;  // sorted rows (tokens) per tile: four 32-row slabs
+constexpr uint32_t kKS = 128;        // inputs per pipeline stage
+constexpr uint32_t kFrags = 1;       // 32-row weight fragments per wave
+constexpr uint32_t kWRows = 4 * kFrags * 32;  // weight rows per block (256)
+constexpr uint32_t kGateUpFeatures = kWRows / 2;  // per gate/up block: 128 gate + 128 up rows
+constexpr uint32_t kDownFeatures = kWRows;        // per down block
 constexpr uint32_t kSharedWord = 0xfffffffeu;  // tile word of the shared expert group
 constexpr uint32_t kDeadWord = 0xffffffffu;    // tile word of rows with invalid route words
 constexpr int kPlanThreads = 1024;
@@ -107,15 +108,51 @@ __global__ void grouped_zero_kernel(uint32_t *p, uint32_t n) {
   if (i < n) p[i] = 0u;
 }
 
+// counter[key] += 1 for every lane with `active`, with one atomic per
+// distinct key in the wave, all issued together (hot experts would otherwise
+// serialize thousands of atomics on one address, and one atomic per loop trip
+// would serialize their latencies).  With WANT_SLOT, returns the lane's slot:
+// the counter's previous value plus the number of lower lanes with its key.
+template <bool WANT_SLOT>
+__device__ __forceinline__ uint32_t wave_aggregated_increment(uint32_t *counter, uint32_t key, bool active) {
+  const int lane = threadIdx.x & 63;
+  uint64_t pending = __ballot(active);
+  int my_leader = lane;
+  uint32_t my_rank = 0u, my_count = 0u;
+  while (pending != 0ull) {  // wave-uniform; one trip per distinct key
+    const int leader = __builtin_ctzll(pending);
+    const uint32_t lkey = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(key), leader));
+    const uint64_t same = __ballot(active && key == lkey) & pending;
+    if ((same >> lane) & 1ull) {
+      my_leader = leader;
+      my_rank = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(same >> 32),
+                                          __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(same), 0u));
+    }
+    if (lane == leader) my_count = static_cast<uint32_t>(__popcll(same));
+    pending &= ~same;
+  }
+  if constexpr (!WANT_SLOT) {
+    if (my_count != 0u) atomicAdd(&counter[key], my_count);
+    return 0u;
+  } else {
+    uint32_t base = 0u;
+    if (my_count != 0u) base = atomicAdd(&counter[key], my_count);
+    base = static_cast<uint32_t>(__shfl(static_cast<int>(base), my_leader, 64));
+    return base + my_rank;
+  }
+}
+
 __global__ void grouped_count_kernel(const uint32_t *__restrict__ routes, uint32_t routed_rows, uint32_t rows,
                                      KeySpace ks, uint32_t *__restrict__ counts, uint32_t *__restrict__ row_key,
                                      unsigned int *__restrict__ err) {
   const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
-  const uint32_t key = r < routed_rows ? key_of(routes[r], ks) : ks.shared_key();
-  if (key == ks.dead_key()) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
-  row_key[r] = key;
-  atomicAdd(&counts[key], 1u);
+  const bool active = r < rows;  // no early return: the whole wave takes part in the aggregation
+  const uint32_t key = !active ? 0u : (r < routed_rows ? key_of(routes[r], ks) : ks.shared_key());
+  if (active) {
+    if (key == ks.dead_key()) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
+    row_key[r] = key;
+  }
+  wave_aggregated_increment<false>(counts, key, active);
 }
 
 // One block: exclusive scans of the rows and tiles per key, the scatter
@@ -168,9 +205,10 @@ __global__ __launch_bounds__(kPlanThreads) void grouped_plan_kernel(const uint32
 __global__ void grouped_scatter_kernel(const uint32_t *__restrict__ row_key, uint32_t rows,
                                        uint32_t *__restrict__ cursor, uint32_t *__restrict__ order) {
   const uint32_t r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
-  const uint32_t pos = atomicAdd(&cursor[row_key[r]], 1u);
-  order[pos] = r;
+  const bool active = r < rows;
+  const uint32_t key = active ? row_key[r] : 0u;
+  const uint32_t pos = wave_aggregated_increment<true>(cursor, key, active);
+  if (active) order[pos] = r;
 }
 
 // ------------------------------------------------------------------ GEMM
@@ -189,110 +227,177 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// One thread's share of one pipeline stage: 32 consecutive inputs (one
-// 16-byte packed weight load, its group's scale and bias) of one weight row,
-// and 32 consecutive inputs (four 16-byte loads) of one activation row.
-struct StageRegs {
-  uint4 w;
-  uint16_t s, b;
-  uint4 x[4];
+// K order inside a stage.  MFMA k-slots can be assigned to inputs in any
+// order as long as both operands agree.  Lane l (fragment row or tile row
+// l%32, half h = l/32) supplies, at k16-step j of a stage, the eight inputs
+// k0 + 64 h + 8 j .. +7: each lane then owns 64 consecutive inputs of its
+// row per stage, i.e. 32 contiguous bytes of packed weights (two 16-byte
+// loads straight into registers, no LDS), and the same 128 contiguous bytes
+// of its activation row.
+
+// Activation tile in LDS: 128 rows x 128 bf16, rows padded by one 16-byte
+// chunk (272 bytes), so the 32 rows of a slab read at one chunk column fall
+// on different banks while every read address is a per-lane base plus an
+// immediate offset.
+constexpr uint32_t kXRow = kKS + 8;  // bf16 per padded LDS row
+__device__ __forceinline__ uint32_t xs_off(uint32_t row, uint32_t chunk) { return row * kXRow + chunk * 8u; }
+
+// Dequantize one packed word (8 consecutive inputs) to bf16(fma(q, s, b)) in
+// MFMA operand order.
+__device__ __forceinline__ bf16x8_t dequant_word(uint32_t w, float s, float b) {
+  const uint32_t lo = w & 0x0f0f0f0fu;         // inputs 0, 2, 4, 6 (one per byte)
+  const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;  // inputs 1, 3, 5, 7
+  const uint4 v = make_uint4(pack_bf16(fmaf(ubyte_to_f32<0>(lo), s, b), fmaf(ubyte_to_f32<0>(hi), s, b)),
+                             pack_bf16(fmaf(ubyte_to_f32<1>(lo), s, b), fmaf(ubyte_to_f32<1>(hi), s, b)),
+                             pack_bf16(fmaf(ubyte_to_f32<2>(lo), s, b), fmaf(ubyte_to_f32<2>(hi), s, b)),
+                             pack_bf16(fmaf(ubyte_to_f32<3>(lo), s, b), fmaf(ubyte_to_f32<3>(hi), s, b)));
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// One lane's weight fragment rows: descriptor (uniform across the wave) and
+// global row (feature), with validity.
+struct WFrag {
+  ExpertRsrc e;
+  uint32_t feature;
+  bool ok;
 };
 
-__device__ __forceinline__ void stage_load(StageRegs &r, const ExpertRsrc &e, bool w_ok, uint32_t feature,
-                                           uint32_t K, uint32_t group, uint32_t k0,
-                                           __amdgpu_buffer_rsrc_t xr, bool x_ok, uint32_t xsrc) {
-  const uint32_t off_w = w_ok ? feature * (K / 2u) + k0 / 2u : kOutOfRange;
-  const uint32_t off_g = w_ok ? (feature * (K / group) + k0 / group) * 2u : kOutOfRange;
-  r.w = buf_load16<kNonTemporal>(e.w, off_w);
-  r.s = buf_load2(e.s, off_g);
-  r.b = buf_load2(e.b, off_g);
-  const uint32_t off_x = x_ok ? (xsrc * K + k0) * 2u : kOutOfRange;
+// A lane's packed weights for one stage and fragment: 64 inputs = 8 words
+// (two 16-byte loads) and the scale/bias of each of their groups (one for
+// group 64, two for group 32).
+struct WRegs {
+  uint4 w[kFrags][2];
+  uint16_t s[kFrags][2], b[kFrags][2];
+};
+
+__device__ __forceinline__ void load_w(WRegs &r, const WFrag (&wf)[kFrags], uint32_t K, uint32_t group,
+                                       uint32_t kbase) {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) r.x[j] = buf_load16(xr, off_x + 16u * j);
+  for (uint32_t f = 0; f < kFrags; ++f)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t k = kbase + 32u * h;
+      const uint32_t off_w = wf[f].ok ? wf[f].feature * (K / 2u) + k / 2u : kOutOfRange;
+      const uint32_t off_g = wf[f].ok ? (wf[f].feature * (K / group) + k / group) * 2u : kOutOfRange;
+      r.w[f][h] = buf_load16(wf[f].e.w, off_w);
+      r.s[f][h] = buf_load2(wf[f].e.s, off_g);
+      r.b[f][h] = buf_load2(wf[f].e.b, off_g);
+    }
 }
 
-// Dequantize the weight part to bf16(fma(q, s, b)) and write both parts to LDS.
-__device__ __forceinline__ void stage_store(const StageRegs &r, uint16_t *ws_row, uint16_t *xs_row) {
-  const float s = bf16_to_f32(r.s), b = bf16_to_f32(r.b);
-  const uint32_t words[4] = {r.w.x, r.w.y, r.w.z, r.w.w};
-  uint32_t pk[16];
+// A thread's share of the activation tile of one stage: 64 inputs (128 bytes)
+// of tile row t/2, half t%2 of the stage.
+struct XRegs {
+  uint4 x[8];
+};
+
+__device__ __forceinline__ void load_x(XRegs &r, __amdgpu_buffer_rsrc_t xr, bool ok, uint32_t src, uint32_t K,
+                                       uint32_t kbase) {
+  const uint32_t off = ok ? (src * K + kbase) * 2u : kOutOfRange;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    // Nibble e of word j is input 8j+e; even nibbles sit in the low halves of
-    // the bytes of `lo`, odd ones in `hi`.
-    const uint32_t lo = words[j] & 0x0f0f0f0fu;
-    const uint32_t hi = (words[j] >> 4) & 0x0f0f0f0fu;
-    pk[4 * j + 0] = pack_bf16(fmaf(ubyte_to_f32<0>(lo), s, b), fmaf(ubyte_to_f32<0>(hi), s, b));
-    pk[4 * j + 1] = pack_bf16(fmaf(ubyte_to_f32<1>(lo), s, b), fmaf(ubyte_to_f32<1>(hi), s, b));
-    pk[4 * j + 2] = pack_bf16(fmaf(ubyte_to_f32<2>(lo), s, b), fmaf(ubyte_to_f32<2>(hi), s, b));
-    pk[4 * j + 3] = pack_bf16(fmaf(ubyte_to_f32<3>(lo), s, b), fmaf(ubyte_to_f32<3>(hi), s, b));
-  }
-  uint4 *wd = reinterpret_cast<uint4 *>(ws_row);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) wd[j] = make_uint4(pk[4 * j], pk[4 * j + 1], pk[4 * j + 2], pk[4 * j + 3]);
-  uint4 *xd = reinterpret_cast<uint4 *>(xs_row);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) xd[j] = r.x[j];
+  for (int j = 0; j < 8; ++j) r.x[j] = buf_load16(xr, off + 16u * j);
 }
 
-// The grouped GEMM core of one work item: C[128 weight rows x 128 rows] over
-// K inputs.  Wave (wr, wt) owns weight rows [64 wr, +64) and tile rows
-// [64 wt, +64) as 2 x 2 MFMA 32x32 tiles.  Thread t stages weight row t/2 and
-// tile row t/2, inputs 32 (t%2) .. +32 of every stage.
+// The grouped GEMM core of one work item: C[256 weight rows x 128 tile rows]
+// over K inputs.  Wave w owns weight rows [64 w, +64) as kFrags fragments
+// (weights dequantized from registers) x 4 slabs of 32 tile rows (activations
+// from LDS); fp32 accumulators.
 struct GemmCore {
-  f32x16_t acc[2][2];
+  f32x16_t acc[kFrags][4];
 };
 
-// `w_lds_row`: the LDS weight row this thread stages (its descriptor `e` must
-// be the same for all lanes of a wave).
-__device__ __forceinline__ void gemm_core(GemmCore &c, uint16_t *ws, uint16_t *xs, const ExpertRsrc &e, bool w_ok,
-                                          uint32_t feature, uint32_t w_lds_row, uint32_t K, uint32_t group,
-                                          __amdgpu_buffer_rsrc_t xr, bool x_ok, uint32_t xsrc, uint32_t count) {
+// One pipeline stage: publish this stage's activations (loaded last stage)
+// to LDS, issue the next stage's loads (weights into `wn`), then run the
+// stage's MFMAs with the weights in `wc` dequantized per k16 step.
+__device__ __forceinline__ void gemm_stage(GemmCore &c, uint16_t *xs, const uint16_t *xs_lane, const WRegs &wc,
+                                           WRegs &wn, XRegs &x, const WFrag (&wf)[kFrags], uint32_t K,
+                                           uint32_t group, __amdgpu_buffer_rsrc_t xr, bool x_ok, uint32_t xsrc,
+                                           uint32_t s, uint32_t stages, uint32_t xrow, uint32_t xhalf, uint32_t half,
+                                           const bool (&slab)[4]) {
+  __syncthreads();  // every wave is done reading the previous activation tile
+#pragma unroll
+  for (int j = 0; j < 8; ++j) *reinterpret_cast<uint4 *>(xs + xs_off(xrow, 8u * xhalf + j)) = x.x[j];
+  __syncthreads();
+  if (s + 1 < stages) {
+    load_w(wn, wf, K, group, (s + 1) * kKS + 64u * half);
+    load_x(x, xr, x_ok, xsrc, K, (s + 1) * kKS + 64u * xhalf);
+  }
+  float sf[kFrags][2], bf[kFrags][2];
+#pragma unroll
+  for (uint32_t f = 0; f < kFrags; ++f)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      sf[f][h] = bf16_to_f32(wc.s[f][h]);
+      bf[f][h] = bf16_to_f32(wc.b[f][h]);
+    }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {  // k16 steps: inputs k0 + 64 half + 8 j
+    bf16x8_t b[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) b[t] = *reinterpret_cast<const bf16x8_t *>(xs_lane + 32u * t * kXRow + 8u * j);
+#pragma unroll
+    for (uint32_t f = 0; f < kFrags; ++f) {
+      const uint4 &q = wc.w[f][j >> 2];
+      const uint32_t word = (j & 3) == 0 ? q.x : (j & 3) == 1 ? q.y : (j & 3) == 2 ? q.z : q.w;
+      const bf16x8_t a = dequant_word(word, sf[f][j >> 2], bf[f][j >> 2]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (slab[t]) c.acc[f][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[t], c.acc[f][t], 0, 0, 0);
+    }
+  }
+}
+
+__device__ __forceinline__ void gemm_core(GemmCore &c, uint16_t *xs, const WFrag (&wf)[kFrags], uint32_t K,
+                                          uint32_t group, __amdgpu_buffer_rsrc_t xr, bool x_ok, uint32_t xsrc,
+                                          uint32_t count) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const uint32_t wave = wave_id();
-  const uint32_t wr = wave & 1u, wt = wave >> 1;
-  const uint32_t half = tid & 1;
-  uint16_t *ws_row = ws + w_lds_row * kLdsK + half * 32u;
-  uint16_t *xs_row = xs + (tid >> 1) * kLdsK + half * 32u;
+  const uint32_t half = static_cast<uint32_t>(lane) >> 5;
+  const uint32_t xrow = static_cast<uint32_t>(tid) >> 1, xhalf = static_cast<uint32_t>(tid) & 1u;
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (uint32_t f = 0; f < kFrags; ++f)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) c.acc[i][j][r] = 0.0f;
-  const bool tok_frag[2] = {wt * 64u < count, wt * 64u + 32u < count};
-  const uint32_t stages = K / kBK;
-  StageRegs st;
-  stage_load(st, e, w_ok, feature, K, group, half * 32u, xr, x_ok, xsrc);
-  for (uint32_t s = 0; s < stages; ++s) {
-    __syncthreads();  // every wave is done reading the previous stage
-    stage_store(st, ws_row, xs_row);
-    __syncthreads();
-    if (s + 1 < stages) stage_load(st, e, w_ok, feature, K, group, (s + 1) * kBK + half * 32u, xr, x_ok, xsrc);
+      for (int r = 0; r < 16; ++r) c.acc[f][j][r] = 0.0f;
+  bool slab[4];
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const uint32_t kcol = kk * 16u + (lane >> 5) * 8u;
-      bf16x8_t a[2], b[2];
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-        a[i] = *reinterpret_cast<const bf16x8_t *>(ws + (wr * 64u + i * 32u + (lane & 31)) * kLdsK + kcol);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-        b[j] = *reinterpret_cast<const bf16x8_t *>(xs + (wt * 64u + j * 32u + (lane & 31)) * kLdsK + kcol);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        if (!tok_frag[j]) continue;  // wave-uniform: no rows in this 32-row slab
-#pragma unroll
-        for (int i = 0; i < 2; ++i) c.acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], c.acc[i][j], 0, 0, 0);
-      }
-    }
+  for (int j = 0; j < 4; ++j) slab[j] = 32u * j < count;
+  const uint32_t stages = K / kKS;
+  WRegs w0, w1;
+  XRegs x;
+  load_w(w0, wf, K, group, 64u * half);
+  load_x(x, xr, x_ok, xsrc, K, 64u * xhalf);
+  const uint16_t *xs_lane = xs + (lane & 31) * kXRow + 64u * half;
+  // Two stages per trip so the weight registers alternate without copies.
+  for (uint32_t s = 0; s < stages; s += 2) {
+    gemm_stage(c, xs, xs_lane, w0, w1, x, wf, K, group, xr, x_ok, xsrc, s, stages, xrow, xhalf, half, slab);
+    if (s + 1 < stages)
+      gemm_stage(c, xs, xs_lane, w1, w0, x, wf, K, group, xr, x_ok, xsrc, s + 1, stages, xrow, xhalf, half, slab);
   }
 }
 
 // C-tile register r of lane l holds weight row 8*(r/4) + 4*(l/32) + r%4 of the
 // 32-row fragment and tile row l%32 of the 32-row slab.
 __device__ __forceinline__ uint32_t c_row(int r, int lane) { return 8u * (r >> 2) + 4u * (lane >> 5) + (r & 3); }
+
+// XCD-aware persistent schedule.  Workgroups are dispatched round-robin over
+// the 8 XCDs (block b runs on XCD b % 8) and each XCD has its own L2.  Tile t
+// is owned by XCD t % 8, and the XCD's blocks walk its (tile, feature block)
+// items in order, so the feature blocks of one tile run at the same time on
+// one XCD and read the tile's activation rows through one L2.  The grid is a
+// multiple of 8 blocks.
+struct XcdItems {
+  uint32_t xcd, first, stride, count, nb_count;
+  __device__ __forceinline__ XcdItems(uint32_t n_tiles, uint32_t nb) : nb_count(nb) {
+    xcd = blockIdx.x & 7u;
+    first = blockIdx.x >> 3;
+    stride = gridDim.x >> 3;
+    const uint32_t tiles_here = n_tiles > xcd ? (n_tiles - xcd + 7u) / 8u : 0u;
+    count = tiles_here * nb;
+  }
+  __device__ __forceinline__ uint32_t tile(uint32_t j) const { return xcd + 8u * (j / nb_count); }
+};
 
 struct GateUpParams {
   const uint16_t *x;
@@ -307,24 +412,21 @@ struct GateUpParams {
   unsigned int *err;
 };
 
-// LDS weight row w (0..127) of a gate/up block: fragment w/32 holds gate
-// features 16*(w/32) + (w%32) for w%32 < 16 and the matching up features for
-// the rest, so a lane's C registers r and r+8 are gate and up of the same
-// feature.
+// Fragment F (0..7) of a gate/up block holds gate features 16 F .. +15 in
+// its rows 0-15 and the matching up features in rows 16-31, so a lane's C
+// registers r and r+8 are gate and up of the same feature.
 __global__ __launch_bounds__(256, 2) void grouped_gateup_kernel(GateUpParams p) {
-  __shared__ __align__(16) uint16_t ws[128 * kLdsK];
-  __shared__ __align__(16) uint16_t xs[kTileRows * kLdsK];
+  __shared__ __align__(16) uint16_t xs[kTileRows * kXRow];
   __shared__ uint32_t row_src[kTileRows];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const uint32_t wave = wave_id();
-  const uint32_t wr = wave & 1u, wt = wave >> 1;
-  const uint32_t nb_count = p.inter / kGateUpFeatures;
-  const uint32_t total = *p.n_tiles * nb_count;
+  const uint32_t nb_count = (p.inter + kGateUpFeatures - 1) / kGateUpFeatures;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.tokens * p.hidden * 2u);
-  for (uint32_t item = blockIdx.x; item < total; item += gridDim.x) {
-    const uint32_t nb = item % nb_count;
-    const GroupTile tile = p.tiles[item / nb_count];
+  const XcdItems it(*p.n_tiles, nb_count);
+  for (uint32_t j = it.first; j < it.count; j += it.stride) {
+    const uint32_t nb = j % nb_count;
+    const GroupTile tile = p.tiles[it.tile(j)];
     __syncthreads();  // the previous item is done with row_src
     if (tid < static_cast<int>(kTileRows)) {
       uint32_t src = ~0u;
@@ -344,30 +446,36 @@ __global__ __launch_bounds__(256, 2) void grouped_gateup_kernel(GateUpParams p) 
     }
     if ((!eg.ok || !eu.ok) && tid == 0 && tile.word != kDeadWord) raise_flag(p.err, MQ_DEVFLAG_BAD_ROUTE);
     __syncthreads();
-    // Waves 0-1 stage the gate rows, waves 2-3 the up rows (one descriptor per wave).
-    const bool is_up = wave >= 2u;
-    const uint32_t f = (static_cast<uint32_t>(tid) & 127u) >> 1;  // feature within the block
-    const uint32_t feature = nb * kGateUpFeatures + f;
-    const uint32_t w_lds_row = 32u * (f >> 4) + (is_up ? 16u : 0u) + (f & 15u);
-    const ExpertRsrc e = is_up ? expert_rsrc(eu, p.inter, p.hidden, p.group) : expert_rsrc(eg, p.inter, p.hidden, p.group);
+    // Lane rows: fragment row (lane % 32) < 16 is a gate row, else an up row.
+    const bool up_half = (lane & 31) >= 16;
+    const ExpertRsrc rg = expert_rsrc(eg, p.inter, p.hidden, p.group);
+    const ExpertRsrc ru = expert_rsrc(eu, p.inter, p.hidden, p.group);
+    WFrag wf[kFrags];
+#pragma unroll
+    for (uint32_t f = 0; f < kFrags; ++f) {
+      const uint32_t frag = wave * kFrags + f;
+      const uint32_t feature = nb * kGateUpFeatures + 16u * frag + (lane & 15);
+      wf[f] = {up_half ? ru : rg, feature, feature < p.inter};
+    }
     const uint32_t xsrc = row_src[static_cast<uint32_t>(tid) >> 1];
     GemmCore c;
-    gemm_core(c, ws, xs, e, feature < p.inter, feature, w_lds_row, p.hidden, p.group, xr, xsrc != ~0u, xsrc,
-              tile.count);
+    gemm_core(c, xs, wf, p.hidden, p.group, xr, xsrc != ~0u, xsrc, tile.count);
     // Epilogue: act = swiglu(bf16(g), bf16(u)) in sorted row order.
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t trow = wt * 64u + j * 32u + (lane & 31);
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t trow = 32u * t + (lane & 31);
       if (trow >= tile.count) continue;
-      uint16_t *dst = p.act + static_cast<uint64_t>(tile.start + trow) * p.inter + nb * kGateUpFeatures;
+      uint16_t *dst = p.act + static_cast<uint64_t>(tile.start + trow) * p.inter;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const uint32_t frag = wr * 2u + i;
+      for (uint32_t f = 0; f < kFrags; ++f) {
+        const uint32_t frag = wave * kFrags + f;
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-          const float g = round_bf16(c.acc[i][j][r]);
-          const float u = round_bf16(c.acc[i][j][r + 8]);
-          dst[16u * frag + c_row(r, lane)] = f32_to_bf16(swiglu_bf16(g, u));
+          const uint32_t feat = nb * kGateUpFeatures + 16u * frag + c_row(r, lane);
+          if (feat >= p.inter) continue;
+          const float g = round_bf16(c.acc[f][t][r]);
+          const float u = round_bf16(c.acc[f][t][r + 8]);
+          dst[feat] = f32_to_bf16(swiglu_bf16(g, u));
         }
       }
     }
@@ -386,20 +494,19 @@ struct DownParams {
   uint32_t routed_rows, hidden, inter, group, dense_count;
 };
 
+// Fragment F (0..7) of a down block holds features 32 F .. +31.
 __global__ __launch_bounds__(256, 2) void grouped_down_kernel(DownParams p) {
-  __shared__ __align__(16) uint16_t ws[128 * kLdsK];
-  __shared__ __align__(16) uint16_t xs[kTileRows * kLdsK];
+  __shared__ __align__(16) uint16_t xs[kTileRows * kXRow];
   __shared__ uint32_t row_dst[kTileRows];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const uint32_t wave = wave_id();
-  const uint32_t wr = wave & 1u, wt = wave >> 1;
-  const uint32_t nb_count = p.hidden / kDownFeatures;
-  const uint32_t total = *p.n_tiles * nb_count;
+  const uint32_t nb_count = (p.hidden + kDownFeatures - 1) / kDownFeatures;
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.act, p.rows * p.inter * 2u);
-  for (uint32_t item = blockIdx.x; item < total; item += gridDim.x) {
-    const uint32_t nb = item % nb_count;
-    const GroupTile tile = p.tiles[item / nb_count];
+  const XcdItems it(*p.n_tiles, nb_count);
+  for (uint32_t j = it.first; j < it.count; j += it.stride) {
+    const uint32_t nb = j % nb_count;
+    const GroupTile tile = p.tiles[it.tile(j)];
     __syncthreads();  // the previous item's epilogue is done with row_dst
     if (tid < static_cast<int>(kTileRows))
       row_dst[tid] = static_cast<uint32_t>(tid) < tile.count ? p.order[tile.start + tid] : ~0u;
@@ -407,28 +514,32 @@ __global__ __launch_bounds__(256, 2) void grouped_down_kernel(DownParams p) {
                               ? expert_ptrs(p.sdown, 0u, p.hidden, p.inter, p.group, 1u)
                               : expert_ptrs(p.down, tile.word, p.hidden, p.inter, p.group, p.dense_count);
     __syncthreads();
-    const uint32_t w = static_cast<uint32_t>(tid) >> 1;
-    const uint32_t feature = nb * kDownFeatures + w;
     const ExpertRsrc e = expert_rsrc(ed, p.hidden, p.inter, p.group);
-    const bool x_ok = w < tile.count;
-    GemmCore c;
-    gemm_core(c, ws, xs, e, feature < p.hidden, feature, w, p.inter, p.group, xr, x_ok, tile.start + w, tile.count);
+    WFrag wf[kFrags];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const uint32_t trow = wt * 64u + j * 32u + (lane & 31);
+    for (uint32_t f = 0; f < kFrags; ++f) {
+      const uint32_t feature = nb * kDownFeatures + 32u * (wave * kFrags + f) + (lane & 31);
+      wf[f] = {e, feature, feature < p.hidden};
+    }
+    const uint32_t xrow = static_cast<uint32_t>(tid) >> 1;
+    GemmCore c;
+    gemm_core(c, xs, wf, p.inter, p.group, xr, xrow < tile.count, tile.start + xrow, tile.count);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t trow = 32u * t + (lane & 31);
       if (trow >= tile.count) continue;
       const uint32_t r = row_dst[trow];
       uint16_t *dst = r < p.routed_rows ? p.y + static_cast<uint64_t>(r) * p.hidden
                                         : p.y_shared + static_cast<uint64_t>(r - p.routed_rows) * p.hidden;
-      dst += nb * kDownFeatures + wr * 64u;
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (uint32_t f = 0; f < kFrags; ++f)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {  // four runs of 4 consecutive features
-          const uint32_t f0 = 32u * i + c_row(4 * q, lane);
-          const uint32_t lo = pack_bf16(c.acc[i][j][4 * q], c.acc[i][j][4 * q + 1]);
-          const uint32_t hi = pack_bf16(c.acc[i][j][4 * q + 2], c.acc[i][j][4 * q + 3]);
-          *reinterpret_cast<uint2 *>(dst + f0) = make_uint2(lo, hi);
+          const uint32_t feat = nb * kDownFeatures + 32u * (wave * kFrags + f) + c_row(4 * q, lane);
+          if (feat >= p.hidden) continue;
+          const uint32_t lo = pack_bf16(c.acc[f][t][4 * q], c.acc[f][t][4 * q + 1]);
+          const uint32_t hi = pack_bf16(c.acc[f][t][4 * q + 2], c.acc[f][t][4 * q + 3]);
+          *reinterpret_cast<uint2 *>(dst + feat) = make_uint2(lo, hi);
         }
     }
   }
@@ -524,8 +635,8 @@ extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
     return fail(MQ_ERR_INVALID, "x, routes and y are required");
   if (a.tokens == 0 || a.slots == 0 || a.slots > 64) return fail(MQ_ERR_INVALID, "tokens must be positive and slots 1..64");
   if (a.group_size != 32 && a.group_size != 64) return fail(MQ_ERR_INVALID, "group_size must be 32 or 64");
-  if (a.hidden % kBK || a.inter % kBK || a.hidden % kDownFeatures || a.inter % kGateUpFeatures)
-    return fail(MQ_ERR_UNSUPPORTED, "grouped path needs hidden %% 128 == 0 and inter %% 64 == 0 (got %u, %u)",
+  if (a.hidden % kKS || a.inter % kKS)
+    return fail(MQ_ERR_UNSUPPORTED, "grouped path needs hidden and inter multiples of %u (got %u, %u)", kKS,
                 a.hidden, a.inter);
   if (a.hidden > MQ_MAX_WIDTH || a.inter > MQ_MAX_WIDTH) return fail(MQ_ERR_INVALID, "width out of bounds");
   int rc;
@@ -577,7 +688,8 @@ extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
   int device = 0, cus = 0;
   MQ_TRY_HIP(hipGetDevice(&device));
   MQ_TRY_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
-  const uint32_t resident = static_cast<uint32_t>(cus > 0 ? cus : 256) * 2u;
+  // One 256-thread block per CU, a multiple of 8 (XCD-aware item schedule).
+  const uint32_t resident = std::max(8u, (static_cast<uint32_t>(cus > 0 ? cus : 256) * 2u / 8u) * 8u);
 
   GateUpParams gp{};
   gp.x = a.x;
@@ -599,8 +711,8 @@ extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
   gp.group = a.group_size;
   gp.dense_count = a.expert_count;
   gp.err = err;
-  const uint32_t gu_items = l.max_tiles * (a.inter / kGateUpFeatures);
-  hipLaunchKernelGGL(grouped_gateup_kernel, dim3(std::min(gu_items, resident)), dim3(256), 0, s, gp);
+  const uint32_t gu_items = l.max_tiles * ceil_div(a.inter, kGateUpFeatures);
+  hipLaunchKernelGGL(grouped_gateup_kernel, dim3(std::min(ceil_div(gu_items, 8) * 8u, resident)), dim3(256), 0, s, gp);
   if ((rc = check_launch("grouped_gateup_kernel"))) return rc;
 
   DownParams dp{};
@@ -618,8 +730,8 @@ extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
   dp.inter = a.inter;
   dp.group = a.group_size;
   dp.dense_count = a.expert_count;
-  const uint32_t dn_items = l.max_tiles * (a.hidden / kDownFeatures);
-  hipLaunchKernelGGL(grouped_down_kernel, dim3(std::min(dn_items, resident)), dim3(256), 0, s, dp);
+  const uint32_t dn_items = l.max_tiles * ceil_div(a.hidden, kDownFeatures);
+  hipLaunchKernelGGL(grouped_down_kernel, dim3(std::min(ceil_div(dn_items, 8) * 8u, resident)), dim3(256), 0, s, dp);
   if ((rc = check_launch("grouped_down_kernel"))) return rc;
 
   if (a.out != nullptr) {
