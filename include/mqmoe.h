@@ -251,10 +251,16 @@ int mq_moe_grouped(const MqGroupedArgs *args, void *stream);
 
 /* ---- expert slot pool refill (models/flashnext/expert_pool.py:112-145) ----
  * Copy n records of record_bytes each from pinned host memory to pool slots
- * on copy_stream, then record done_event (if not NULL) on that stream.
+ * (slot i lands at pool + pool_header + slots[i] * pool_stride) on
+ * copy_stream, then record done_event (if not NULL) on that stream.  The
+ * reference reads the nine rows of each missed expert into its slot; here a
+ * host record already holds the nine parts at their layout offsets.
  * `slots` and `host_records` are HOST arrays of n entries; each
- * host_records[i] must be host-pinned memory (hipHostMalloc). */
-int mq_pool_refill_async(uint8_t *pool, uint64_t pool_header, uint64_t pool_stride,
+ * host_records[i] must be host-pinned memory (hipHostMalloc).  Slots at or
+ * beyond pool_slots are rejected.  The caller orders the copies after the
+ * last kernel that reads a refilled slot (an event wait on copy_stream) and
+ * makes consumers wait on done_event. */
+int mq_pool_refill_async(uint8_t *pool, uint64_t pool_header, uint64_t pool_stride, uint32_t pool_slots,
                          const uint32_t *slots, const void *const *host_records,
                          uint32_t n, uint64_t record_bytes, void *copy_stream,
                          void *done_event);

@@ -148,7 +148,7 @@ extern "C" int mq_record_layout(uint32_t hidden, uint32_t inter, uint32_t group_
   return MQ_OK;
 }
 
-extern "C" int mq_pool_refill_async(uint8_t *pool, uint64_t pool_header, uint64_t pool_stride,
+extern "C" int mq_pool_refill_async(uint8_t *pool, uint64_t pool_header, uint64_t pool_stride, uint32_t pool_slots,
                                     const uint32_t *slots, const void *const *host_records, uint32_t n,
                                     uint64_t record_bytes, void *copy_stream, void *done_event) {
   if (n == 0) {
@@ -160,8 +160,12 @@ extern "C" int mq_pool_refill_async(uint8_t *pool, uint64_t pool_header, uint64_
   if (record_bytes == 0 || record_bytes > pool_stride)
     return fail(MQ_ERR_INVALID, "record_bytes must be in 1..pool_stride");
   hipStream_t s = static_cast<hipStream_t>(copy_stream);
-  for (uint32_t i = 0; i < n; ++i) {
+  for (uint32_t i = 0; i < n; ++i) {  // validate everything before the first copy
     if (host_records[i] == nullptr) return fail(MQ_ERR_INVALID, "host record %u is NULL", i);
+    if ((slots[i] & 0x7fffffffu) >= pool_slots)
+      return fail(MQ_ERR_INVALID, "slot %u is outside the pool (%u slots)", slots[i] & 0x7fffffffu, pool_slots);
+  }
+  for (uint32_t i = 0; i < n; ++i) {
     uint8_t *dst = pool + pool_header + static_cast<uint64_t>(slots[i] & 0x7fffffffu) * pool_stride;
     MQ_TRY_HIP(hipMemcpyAsync(dst, host_records[i], record_bytes, hipMemcpyHostToDevice, s));
   }

@@ -168,7 +168,7 @@ def _declare(lib) -> None:
         "mq_moe_layer": ([c.POINTER(MqRouteArgs), c.POINTER(MqMoeArgs), vp], i32),
         "mq_grouped_workspace_size": ([u32, u32, u32, u32, u32, i32], u64),
         "mq_moe_grouped": ([c.POINTER(MqGroupedArgs), vp], i32),
-        "mq_pool_refill_async": ([vp, u64, u64, vp, vp, u32, u64, vp, vp], i32),
+        "mq_pool_refill_async": ([vp, u64, u64, u32, vp, vp, u32, u64, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

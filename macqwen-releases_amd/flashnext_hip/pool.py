@@ -1,0 +1,159 @@
+"""HBM expert slot pool with LRU assignment and pinned-host refill.
+
+Mirrors ``models/flashnext/expert_pool.py`` (``ExpertPool``): one region
+laid out like the slab pack (a 4 KiB header, then fixed-stride records with
+the nine parts at the layout offsets), an LRU over ``(layer, expert)`` keys
+(:meth:`HipExpertPool.assign` restates ``assign`` ``:88-110``: hits move to
+the most recent end first, then every miss takes a free slot, ascending from
+slot 0, or evicts the least recently used key), and a fill of the missed
+records (``fill`` ``:133-145``).
+
+The region is HBM (a device tensor), the decode and grouped kernels address
+its records in place through slot words (``0x80000000 | slot``), and a miss
+is one pinned host-to-device copy of the whole record image on a side stream
+(``mq_pool_refill_async``) instead of nine file reads.  Ordering follows the
+reference's rule that a slot is only overwritten after its last reader
+finished: the copy stream first waits for everything already queued on the
+compute stream, and the compute stream then waits for the copies.
+"""
+from __future__ import annotations
+
+import ctypes
+from collections import OrderedDict
+
+import torch
+
+from . import _lib
+from .layout import HEADER_SIZE, PART_KEYS, SlabLayout, make_layout
+
+SLOT_BIT = _lib.MQ_SLOT_BIT
+MIN_SLOTS = 16  # one decode layer (expert_pool.py:64-65)
+
+
+class HostRecordStore:
+    """Record images of experts in pinned host memory, keyed by (layer, expert).
+
+    Each image is ``record_stride`` bytes with the nine parts at their layout
+    offsets, so one contiguous copy places a whole record in a pool slot.
+    """
+
+    def __init__(self, layout: SlabLayout):
+        self.layout = layout
+        self._records: dict[tuple[int, int], torch.Tensor] = {}
+
+    def add(self, layer: int, expert: int, parts: dict) -> None:
+        """``parts``: ``"gate_proj.weight" -> tensor`` (any dtype, host or device)."""
+        img = torch.zeros(self.layout.record_stride, dtype=torch.uint8, pin_memory=True)
+        for proj, part in PART_KEYS:
+            data = parts[f"{proj}.{part}"].detach().contiguous().view(torch.uint8).reshape(-1).cpu()
+            off = self.layout.offset(proj, part)
+            img[off:off + data.numel()].copy_(data)
+        self._records[(int(layer), int(expert))] = img
+
+    def add_banks(self, layer: int, banks: dict) -> None:
+        """``banks``: ``"gate_proj" -> (weight [E,...], scales, biases)``; adds every expert."""
+        experts = banks["gate_proj"][0].shape[0]
+        for e in range(experts):
+            parts = {}
+            for proj in ("gate_proj", "up_proj", "down_proj"):
+                w, s, b = banks[proj]
+                parts[f"{proj}.weight"], parts[f"{proj}.scales"], parts[f"{proj}.biases"] = w[e], s[e], b[e]
+            self.add(layer, e, parts)
+
+    def record(self, layer: int, expert: int) -> torch.Tensor:
+        try:
+            return self._records[(int(layer), int(expert))]
+        except KeyError:
+            raise KeyError(f"no host record for layer {layer} expert {expert}") from None
+
+
+class HipExpertPool:
+    """LRU pool of expert records resident in HBM."""
+
+    def __init__(self, size_bytes: int, hidden: int, inter: int, group_size: int = 32, *, device="cuda"):
+        self.layout = make_layout(hidden, inter, group_size)
+        self.stride = self.layout.record_stride
+        self.slots = (int(size_bytes) - HEADER_SIZE) // self.stride
+        if self.slots < MIN_SLOTS:
+            raise ValueError("expert pool is too small for one decode layer")
+        self.buffer = torch.zeros(HEADER_SIZE + self.slots * self.stride, dtype=torch.uint8, device=device)
+        self._slot_of: "OrderedDict[tuple, int]" = OrderedDict()
+        self._free = list(range(self.slots - 1, -1, -1))
+        self.hits = 0
+        self.misses = 0
+        self._lib = _lib.load()
+
+    # ------------------------------------------------------------ LRU (expert_pool.py:88-110)
+    def assign(self, layer: int, experts):
+        """Return ``({expert: slot}, [(expert, slot) to fill])`` for one layer."""
+        slot_of = self._slot_of
+        slots, misses = {}, []
+        for expert in experts:
+            key = (layer, expert)
+            slot = slot_of.get(key)
+            if slot is not None:
+                slot_of.move_to_end(key)
+                slots[expert] = slot
+        self.hits += len(slots)
+        for expert in experts:
+            if expert in slots:
+                continue
+            if self._free:
+                slot = self._free.pop()
+            else:
+                _old, slot = slot_of.popitem(last=False)
+            slot_of[(layer, expert)] = slot
+            slots[expert] = slot
+            misses.append((expert, slot))
+        self.misses += len(misses)
+        return slots, misses
+
+    # ------------------------------------------------------------ refill (expert_pool.py:112-145)
+    def fill(self, layer: int, misses, store: HostRecordStore, *, compute_stream=None, copy_stream=None):
+        """Copy the missed records from pinned host memory into their slots.
+
+        The copies run on ``copy_stream`` after everything already queued on
+        ``compute_stream`` (earlier readers of the victim slots); the compute
+        stream then waits for them.  Returns the completion event.
+        """
+        compute = compute_stream if compute_stream is not None else torch.cuda.current_stream(self.buffer.device)
+        copy = copy_stream if copy_stream is not None else compute
+        done = torch.cuda.Event()
+        if copy is not compute:
+            copy.wait_stream(compute)
+        n = len(misses)
+        slots = (ctypes.c_uint32 * max(n, 1))(*[int(slot) for _e, slot in misses])
+        recs = [store.record(layer, e) for e, _slot in misses]  # owned by the store: outlive the copies
+        ptrs = (ctypes.c_void_p * max(n, 1))(*[r.data_ptr() for r in recs])
+        rc = self._lib.mq_pool_refill_async(
+            ctypes.c_void_p(self.buffer.data_ptr()), HEADER_SIZE, self.stride, self.slots, slots, ptrs, n,
+            self.stride, ctypes.c_void_p(copy.cuda_stream), None)
+        _lib.check(rc, self._lib)
+        done.record(copy)
+        compute.wait_event(done)
+        return done
+
+    # ------------------------------------------------------------ addressing
+    def projection(self, name: str) -> _lib.MqProjection:
+        p = _lib.MqProjection()
+        p.pool = self.buffer.data_ptr()
+        p.pool_header = HEADER_SIZE
+        p.pool_stride = self.stride
+        p.pool_slots = self.slots
+        p.off_weight = self.layout.offset(name, "weight")
+        p.off_scales = self.layout.offset(name, "scales")
+        p.off_biases = self.layout.offset(name, "biases")
+        return p
+
+    @staticmethod
+    def route_words(slots: dict, inds) -> torch.Tensor:
+        """Slot words ``0x80000000 | slot`` (as int32 bits) for an expert-id tensor."""
+        import numpy as np
+
+        flat = np.array([SLOT_BIT | slots[int(e)] for e in inds.reshape(-1).tolist()], dtype=np.uint32)
+        return torch.from_numpy(flat.view(np.int32).reshape(tuple(inds.shape)))
+
+    def record_bytes(self, slot: int) -> torch.Tensor:
+        """Device view of one slot's record (for checks)."""
+        base = HEADER_SIZE + int(slot) * self.stride
+        return self.buffer[base:base + self.stride]

@@ -1,0 +1,110 @@
+"""Expert slot pool: LRU assignment against the reference KAT and the oracle
+(CPU), and byte-exact pinned-host refills addressed by the decode kernels
+(GPU)."""
+from __future__ import annotations
+
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from oracle import pool as opool
+
+KATS = json.loads((Path(__file__).parent / "golden" / "reference_kats.json").read_text())
+
+
+def _pool_cpu(slots, hidden=2048, inter=512):
+    from flashnext_hip.pool import HEADER_SIZE, HipExpertPool, make_layout
+
+    stride = make_layout(hidden, inter).record_stride
+    return HipExpertPool(HEADER_SIZE + slots * stride, hidden, inter, device="cpu")
+
+
+def test_pool_assign_reference_kat():
+    """models/flashnext/tests/unit/test_expert_pool.py:32-49."""
+    pool = _pool_cpu(16)
+    slots, misses = pool.assign(1, list(range(10)))
+    assert len(misses) == 10 and len(set(slots.values())) == 10
+    slots2, misses2 = pool.assign(1, [3, 4, 20])
+    assert slots2[3] == slots[3] and [e for e, _ in misses2] == [20]
+    pool.assign(2, list(range(5)))
+    slots3, misses3 = pool.assign(1, [3, 4, 30, 31])
+    assert slots3[3] == slots[3] and slots3[4] == slots[4]
+    assert {slot for _, slot in misses3} == {slots[0], slots[1]}
+    assert pool.hits == 4 and pool.misses == 10 + 1 + 5 + 2
+
+
+def test_pool_too_small_is_refused():
+    with pytest.raises(ValueError):
+        _pool_cpu(4)
+
+
+def test_pool_assign_matches_oracle_on_random_traffic():
+    rng = np.random.default_rng(11)
+    pool, lru = _pool_cpu(40), opool.LruSlots(40)
+    for step in range(300):
+        layer = int(rng.integers(0, 6))
+        experts = [int(e) for e in rng.choice(64, size=int(rng.integers(1, 12)), replace=False)]
+        assert pool.assign(layer, experts) == lru.assign(layer, experts), step
+    assert (pool.hits, pool.misses) == (lru.hits, lru.misses)
+
+
+def test_pool_assign_golden_calls():
+    kat = KATS["lru_assign"]
+    pool = _pool_cpu(kat["slots"])
+    lru = opool.LruSlots(kat["slots"])
+    for layer, experts in kat["calls"]:
+        assert pool.assign(layer, experts) == lru.assign(layer, experts)
+
+
+@pytest.mark.gpu
+def test_pool_refill_bytes_and_decode_through_slots():
+    import torch
+
+    from flashnext_hip import _lib
+    from flashnext_hip.hip_runtime import HipMoEExecutor
+    from flashnext_hip.pool import HEADER_SIZE, HipExpertPool, HostRecordStore
+
+    from ._helpers import bf16_normal, make_records, say, to_dev_bank, to_dev_bf16
+
+    assert torch.cuda.is_available()
+    say("case: pool refill + decode via slot words")
+    H, I, E = 1024, 256, 12
+    rec = make_records(E, H, I, seed=400)
+    banks = {n: to_dev_bank(b) for n, b in (("gate_proj", rec.gate), ("up_proj", rec.up), ("down_proj", rec.down))}
+    pool = HipExpertPool(HEADER_SIZE + 16 * _lib.record_layout(H, I)[1], H, I)
+    store = HostRecordStore(pool.layout)
+    store.add_banks(3, banks)
+    copy = torch.cuda.Stream()
+    experts = [7, 2, 9, 0, 11]
+    slots, misses = pool.assign(3, experts)
+    pool.fill(3, misses, store, copy_stream=copy)
+    torch.cuda.synchronize()
+    for e, slot in misses:
+        assert torch.equal(pool.record_bytes(slot).cpu(), store.record(3, e)), (e, slot)
+    # decode two tokens through slot words == through dense expert ids
+    tokens, k = 2, 4
+    x = to_dev_bf16(bf16_normal((tokens, H), seed=401))
+    inds = torch.tensor([[7, 2, 9, 0], [11, 9, 7, 2]], dtype=torch.int64)
+    scores = torch.full((tokens, k), 0.25, device="cuda")
+    ex = HipMoEExecutor(E, H, k, max_tokens=8)
+    dense = ex.execute(x, inds.cuda(), banks, scores=scores)
+    words = HipExpertPool.route_words(slots, inds).cuda()
+    pooled = ex.execute(x, words, banks, scores=scores, slab_pack=pool.buffer)
+    assert torch.equal(dense.view(torch.int16), pooled.view(torch.int16))
+    # evict and refill: 16 slots, 5 used; 14 new experts of another layer evict the oldest
+    store.add_banks(4, banks)
+    slots4, misses4 = pool.assign(4, list(range(11)) + [0, 1, 2])
+    pool.fill(4, misses4, store, copy_stream=copy)
+    torch.cuda.synchronize()
+    for e, slot in misses4:
+        assert torch.equal(pool.record_bytes(slot).cpu(), store.record(4, e))
+    with pytest.raises(ValueError):  # a slot outside the pool is rejected before any copy
+        lib = _lib.load()
+        import ctypes
+
+        bad = (ctypes.c_uint32 * 1)(pool.slots)
+        ptrs = (ctypes.c_void_p * 1)(store.record(4, 0).data_ptr())
+        _lib.check(lib.mq_pool_refill_async(ctypes.c_void_p(pool.buffer.data_ptr()), HEADER_SIZE, pool.stride,
+                                            pool.slots, bad, ptrs, 1, pool.stride, None, None), lib)
