@@ -6,7 +6,8 @@ Drop-in for the reference's ``models/flashnext`` expert path:
 * ``ops``          ``quantized_matmul`` / ``gather_qmm`` / ``dequantize``
 * ``router``       softmax / top-k / renorm / slot words on the device
 * ``moe_block``    the ``_moe_call`` composition (router + experts + shared)
-* ``expert_pool``  HBM-resident slot pool with LRU and pinned-host refill
+* ``grouped``      prefill / verify grouped path (sorted rows, MFMA GEMMs)
+* ``pool``         HBM-resident slot pool with LRU and pinned-host refill
 * ``layout``       the expert record layout
 * ``_lib``         ctypes binding of ``libmqmoe.so`` (``include/mqmoe.h``)
 

@@ -10,7 +10,7 @@ the rows are unsorted, and ``_moe_call`` combines the slots in bf16
 
 :func:`grouped_moe` does the same in one C-ABI call (``mq_moe_grouped``): a
 counting sort on the device, bf16 MFMA grouped GEMMs with the weights
-dequantized in LDS, and the bf16 combine.  The shared expert may be given
+dequantized in registers, and the bf16 combine.  The shared expert may be given
 precomputed (``shared``) or as a dense single-expert bank
 (``shared_expert``), which then runs as one more group over all tokens.
 """

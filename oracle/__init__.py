@@ -38,4 +38,17 @@ PINNING = {
     "moe.down_combine": "closed form on exactly representable values; slot-order invariance on exact sums",
     "pool.record_layout": "reference constants test_slab_pack.py:50-63 (3,072,000 stride and offsets)",
     "pool.LruSlots": "reference KAT test_expert_pool.py:32-49 (hits 4, misses 18, evicted slot0/slot1)",
+    "router.router_logits": "closed form: integer-valued bf16 inputs give exact dot products, rounded once",
+    "router.adaptive_keep/pad_dropped": "hand KAT of adaptive_topk.py:43-50, 213-227 (keep, padding, width)",
+    "moe.generic_combine": "closed form on exactly representable values (bf16 products, slot-order f32 sum)",
+    "q4.ExpertBank.dense_bf16": "closed form: equals bf16(float32(exact dequant)); within half a bf16 ulp",
+    "moe.decode_layer / moe.prefill_layer": "compositions of the pinned parts above; decode_layer "
+                                            "cross-checked against the independent C restatement",
+    "c.mqo_decode_layer / c.mqo_qmv": "cross-checked against the numpy restatement (tests/test_oracle_c.py)",
 }
+# Functions whose values only MLX itself could fix (parity unpinned at the MLX
+# boundary): MLX's own qmv/gather_qmm fp32 reduction order and bf16 output
+# bits, argpartition tie order, softmax(precise=True) last-ulp behaviour and
+# the bf16 rounding inside mx.exp.  The oracle fixes these as exact rounding
+# (float64 accumulation rounded once; correctly rounded exp; ties to the lower
+# expert index).

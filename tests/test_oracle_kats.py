@@ -286,3 +286,17 @@ def test_bf16_tile_weights_are_rounded_exact_weights():
         assert np.array_equal(tiles, bf16_to_f32(f32_to_bf16(exact.astype(np.float32))).astype(np.float64))
         # a bf16 tile differs from the exact weight by at most half a bf16 ulp
         assert np.all(np.abs(tiles - exact) <= np.abs(exact) * 2.0 ** -8 + 1e-30)
+
+
+def test_router_logits_exact_rounding():
+    """x @ Wg.T accumulated exactly and rounded once: with small integer-valued
+    bf16 inputs the dot products are exact integers, so the bf16 logits must be
+    the bf16 rounding of the integer dot product (odd sums exercise ties)."""
+    rng = np.random.default_rng(12)
+    x = rng.integers(-8, 9, (3, 64)).astype(np.float32)
+    w = rng.integers(-8, 9, (5, 64)).astype(np.float32)
+    got = router.router_logits(bf16.f32_to_bf16(x), bf16.f32_to_bf16(w))
+    want = bf16.f32_to_bf16((x.astype(np.float64) @ w.T.astype(np.float64)).astype(np.float32))
+    assert np.array_equal(got, want)
+    big = np.full((1, 64), 3.0, np.float32)  # 64 * 3 * 3 = 576 -> bf16 576 exactly; 577 -> tie case below
+    assert bf16.bf16_to_f32(router.router_logits(bf16.f32_to_bf16(big), bf16.f32_to_bf16(big)))[0, 0] == 576.0
