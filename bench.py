@@ -198,6 +198,160 @@ def prefill_bench(torch, dev, reps: int = 10) -> dict:
             "note": "sort + grouped MFMA GEMMs + bf16 combine timed together; routed experts only"}
 
 
+def qmv_bench(torch, dev, lib, stream, copies: int = 64, reps: int = 50) -> dict:
+    """Single Q4/g32 QMV, x bf16 [1,2048] times W [5120,2048]^T, through
+    ``mq_q4_qmv``; ``copies`` distinct weight matrices (about 420 MB) are
+    stepped through in a graph so the bytes come from HBM."""
+    from flashnext_hip import _lib
+    from flashnext_hip.synthetic import make_bank
+
+    out_w, in_w = 5120, HIDDEN
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5120)
+    bank = make_bank(copies, out_w, in_w, gen, dev, group=GROUP, chunk=8)
+    x = torch.randn((1, in_w), generator=gen, device=dev).to(torch.bfloat16)
+    y = torch.empty((copies, out_w), dtype=torch.bfloat16, device=dev)
+    torch.cuda.synchronize()
+    handle = stream.cuda_stream
+
+    def run():
+        for c in range(copies):
+            rc = lib.mq_q4_qmv(x.data_ptr(), _lib.MQ_BF16, bank.weight[c].data_ptr(), bank.scales[c].data_ptr(),
+                               bank.biases[c].data_ptr(), y[c].data_ptr(), 1, out_w, in_w, GROUP, handle)
+            if rc:
+                _lib.check(rc, lib)
+
+    with torch.cuda.stream(stream):
+        run()
+    torch.cuda.synchronize()
+    g = capture(torch, run, stream)
+    time_graph(torch, g, 3, stream)
+    ms = time_graph(torch, g, reps, stream) / (reps * copies)
+    nbytes = out_w * in_w // 2 + 2 * 2 * out_w * in_w // GROUP + 2 * in_w + 2 * out_w
+    # check one product against a float64 dequantised matmul (bf16 output rounding)
+    wq = bank.weight[0].view(torch.int32)
+    shifts = 4 * torch.arange(8, device=dev, dtype=torch.int32)
+    q = ((wq[..., None] >> shifts) & 15).reshape(out_w, in_w).double()
+    s = bank.scales[0].double().repeat_interleave(GROUP, dim=1)
+    b = bank.biases[0].double().repeat_interleave(GROUP, dim=1)
+    want = ((s * q + b) @ x[0].double())
+    got = y[0].double()
+    del bank, g
+    return {"workload": f"Q4 g{GROUP} QMV [1,{in_w}] x [{out_w},{in_w}]^T, {copies} distinct weight copies in a graph",
+            "us": round(ms * 1000, 3), "bytes": nbytes, "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "max_rel": float((got - want).abs().max() / want.abs().max())}
+
+
+def verify_bench(torch, dev, runners, stream, tokens: int, reps: int = 10) -> dict:
+    """Small-batch decode / speculative verify: ``tokens`` independent rows per
+    layer over the same rotating layers; bytes are the exact unique routed
+    experts of each layer's seeded routes plus the shared expert."""
+    from flashnext_hip import _lib
+    from flashnext_hip.moe_block import DecodeLayer
+
+    handle = stream.cuda_stream
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1000 + tokens)
+    rs = []
+    for r in runners:
+        v = DecodeLayer(r.w, tokens, TOP_K, device=dev)
+        v.x.copy_(torch.randn(v.x.shape, generator=gen, device=dev).to(torch.bfloat16))
+        rs.append(v)
+    fused = tokens <= 8  # the routed-layer entry point takes up to 8 tokens
+
+    def run():
+        for v in rs:
+            (v.launch if fused else v.launch_unfused)(handle)
+
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        run()
+    _lib.check_device_errors(handle)
+    unique = [len(set(v.inds.cpu().reshape(-1).tolist())) for v in rs]
+    g = capture(torch, run, stream)
+    time_graph(torch, g, 2, stream)
+    ms = time_graph(torch, g, reps, stream) / (reps * len(rs))
+    nbytes = (sum(unique) / len(unique) + 1) * expert_bytes_per_record()
+    del g, rs
+    return {"tokens": tokens, "path": "mq_moe_layer" if fused else "mq_route_topk + mq_moe_decode",
+            "us_per_layer": round(ms * 1000, 3), "us_per_token": round(ms * 1000 / tokens, 3),
+            "unique_experts_mean": round(sum(unique) / len(unique), 2), "expert_bytes_per_layer": int(nbytes),
+            "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def stack_bench(torch, dev, runners, stream, steps: int = 128) -> dict:
+    """48 stacked MoE blocks, ``steps`` decode steps, each with a fresh N(0,1)
+    hidden state per layer written into the layers' inputs before the step."""
+    from flashnext_hip import _lib
+    from flashnext_hip.moe_block import DecodeLayer
+
+    handle = stream.cuda_stream
+    L = len(runners)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(128)
+    xbuf = torch.zeros((L, 1, HIDDEN), dtype=torch.bfloat16, device=dev)
+    xs = torch.randn((steps, L, 1, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
+    rs = [DecodeLayer(r.w, 1, TOP_K, device=dev, x=xbuf[l]) for l, r in enumerate(runners)]
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for v in rs:
+            v.launch(handle)
+    _lib.check_device_errors(handle)
+    g = capture(torch, lambda: [v.launch(handle) for v in rs], stream)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        xbuf.copy_(xs[0])
+        g.replay()  # warm
+        start.record(stream)
+        for s in range(steps):
+            xbuf.copy_(xs[s])
+            g.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    nbytes = L * (TOP_K + 1) * expert_bytes_per_record()
+    del g, rs
+    return {"workload": f"{L} stacked MoE blocks, {steps} decode steps, fresh N(0,1) hidden per step and layer, "
+                        f"{L * EXPERTS} expert records in the HBM pool",
+            "us_per_token": round(ms * 1000, 2), "expert_bytes_per_token": nbytes,
+            "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "router_bytes_per_token": L * EXPERTS * HIDDEN * 2}
+
+
+def peaks_bench(torch, dev) -> dict:
+    """Measured ceilings on this GPU: a 1 GiB device copy and a bf16 GEMM."""
+    a = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(2):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(10):
+        b.copy_(a)
+    end.record()
+    torch.cuda.synchronize()
+    copy_gbps = 2 * a.numel() * 10 / (start.elapsed_time(end) * 1e-3) / 1e9
+    del a, b
+    n = 8192
+    m1 = torch.randn((n, n), device=dev).to(torch.bfloat16)
+    m2 = torch.randn((n, n), device=dev).to(torch.bfloat16)
+    for _ in range(3):
+        torch.matmul(m1, m2)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(20):
+        torch.matmul(m1, m2)
+    end.record()
+    torch.cuda.synchronize()
+    tflops = 2 * n ** 3 * 20 / (start.elapsed_time(end) * 1e-3) / 1e12
+    return {"copy_gbps": round(copy_gbps, 1), "bf16_gemm_tflops_8192": round(tflops, 1),
+            "note": "device-to-device copy counts read + write bytes; GEMM through torch.matmul (hipBLASLt)"}
+
+
 def load_traffic(kernel_tag: str):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if present."""
     path = ROOT / "profiles" / f"{kernel_tag}_pmc.md"
@@ -234,6 +388,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="skip the QMV / verify / stack / peak rows")
     ap.add_argument("--pmc-pass", action="store_true", help="eager launches for rocprofv3 --pmc, no timing")
     ap.add_argument("--prefill-only", action="store_true", help="time only the 4096-token prefill grouped path")
     args = ap.parse_args()
@@ -313,6 +468,17 @@ def main() -> int:
 
     check = check_layer0(torch, layers[0], runners[0])
     log(f"check layer0: {check}")
+    extras = {}
+    if not args.no_extras:
+        log("timing the QMV, small-batch verify and 48-block stack workloads")
+        extras["qmv"] = qmv_bench(torch, dev, lib, stream)
+        log(f"qmv: {extras['qmv']}")
+        extras["verify"] = [verify_bench(torch, dev, runners, stream, t) for t in (4, 16)]
+        log(f"verify: {extras['verify']}")
+        extras["stack"] = stack_bench(torch, dev, runners, stream)
+        log(f"stack: {extras['stack']}")
+        extras["peaks_measured"] = peaks_bench(torch, dev)
+        log(f"peaks: {extras['peaks_measured']}")
     prefill = None
     if not args.no_prefill:
         log("timing the 4096-token prefill grouped path")
@@ -351,6 +517,7 @@ def main() -> int:
                      "frac": round(exp_gbps / HBM_PEAK_GBPS, 4), "traffic": load_traffic("decode_expert_stage"),
                      "algorithmic_bytes_per_launch": expert_bytes, "us_per_launch": round(exp_ms * 1000, 3)},
         "prefill": prefill,
+        **extras,
         "cpu_baseline": cpu,
         "check": check,
     }

@@ -32,10 +32,13 @@ namespace {
 
 constexpr uint32_t kTileRows = 128;  // sorted rows (tokens) per tile: four 32-row slabs
 constexpr uint32_t kKS = 128;        // inputs per pipeline stage
-constexpr uint32_t kFrags = 1;       // 32-row weight fragments per wave
-constexpr uint32_t kWRows = 4 * kFrags * 32;  // weight rows per block (256)
-constexpr uint32_t kGateUpFeatures = kWRows / 2;  // per gate/up block: 128 gate + 128 up rows
-constexpr uint32_t kDownFeatures = kWRows;        // per down block
+constexpr uint32_t kGemmWaves = 8;                      // waves per GEMM block (one block per CU)
+constexpr uint32_t kGemmThreads = 64 * kGemmWaves;
+constexpr uint32_t kWRows = kGemmWaves * 32;            // weight rows per block: 32 per wave
+constexpr uint32_t kGateUpFeatures = kWRows / 2;        // per gate/up block: 128 gate + 128 up rows
+constexpr uint32_t kDownFeatures = kWRows;              // per down block
+constexpr uint32_t kXParts = kGemmThreads / kTileRows;  // threads per activation row of a stage
+constexpr uint32_t kXChunks = kKS / 8 / kXParts;        // 16-byte chunks per thread and stage
 constexpr uint32_t kSharedWord = 0xfffffffeu;  // tile word of the shared expert group
 constexpr uint32_t kDeadWord = 0xffffffffu;    // tile word of rows with invalid route words
 constexpr int kPlanThreads = 1024;
@@ -254,126 +257,114 @@ __device__ __forceinline__ bf16x8_t dequant_word(uint32_t w, float s, float b) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
-// One lane's weight fragment rows: descriptor (uniform across the wave) and
-// global row (feature), with validity.
-struct WFrag {
+constexpr uint32_t kXTile = kTileRows * kXRow;  // bf16 per LDS activation tile
+
+// One lane's weights for one stage: 64 inputs of its weight row as 8 packed
+// words (two 16-byte loads) and the scales and biases of their groups.  Group
+// 32: two bf16 in one 32-bit load (words 0-3 use the low half, words 4-7 the
+// high half); group 64: one bf16 for all eight words.
+struct WStage {
+  uint4 w[2];
+  uint32_t s, b;
+};
+
+// The weight row a lane streams for one work item: the wave's projection
+// descriptors (wave-uniform, so the loads need no per-lane descriptor) and
+// the lane's row.
+struct WRow {
   ExpertRsrc e;
-  uint32_t feature;
+  uint32_t row;
   bool ok;
 };
 
-// A lane's packed weights for one stage and fragment: 64 inputs = 8 words
-// (two 16-byte loads) and the scale/bias of each of their groups (one for
-// group 64, two for group 32).
-struct WRegs {
-  uint4 w[kFrags][2];
-  uint16_t s[kFrags][2], b[kFrags][2];
-};
-
-__device__ __forceinline__ void load_w(WRegs &r, const WFrag (&wf)[kFrags], uint32_t K, uint32_t group,
-                                       uint32_t kbase) {
-#pragma unroll
-  for (uint32_t f = 0; f < kFrags; ++f)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const uint32_t k = kbase + 32u * h;
-      const uint32_t off_w = wf[f].ok ? wf[f].feature * (K / 2u) + k / 2u : kOutOfRange;
-      const uint32_t off_g = wf[f].ok ? (wf[f].feature * (K / group) + k / group) * 2u : kOutOfRange;
-      r.w[f][h] = buf_load16(wf[f].e.w, off_w);
-      r.s[f][h] = buf_load2(wf[f].e.s, off_g);
-      r.b[f][h] = buf_load2(wf[f].e.b, off_g);
-    }
-}
-
-// A thread's share of the activation tile of one stage: 64 inputs (128 bytes)
-// of tile row t/2, half t%2 of the stage.
-struct XRegs {
-  uint4 x[8];
-};
-
-__device__ __forceinline__ void load_x(XRegs &r, __amdgpu_buffer_rsrc_t xr, bool ok, uint32_t src, uint32_t K,
-                                       uint32_t kbase) {
-  const uint32_t off = ok ? (src * K + kbase) * 2u : kOutOfRange;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) r.x[j] = buf_load16(xr, off + 16u * j);
-}
-
-// The grouped GEMM core of one work item: C[256 weight rows x 128 tile rows]
-// over K inputs.  Wave w owns weight rows [64 w, +64) as kFrags fragments
-// (weights dequantized from registers) x 4 slabs of 32 tile rows (activations
-// from LDS); fp32 accumulators.
-struct GemmCore {
-  f32x16_t acc[kFrags][4];
-};
-
-// One pipeline stage: publish this stage's activations (loaded last stage)
-// to LDS, issue the next stage's loads (weights into `wn`), then run the
-// stage's MFMAs with the weights in `wc` dequantized per k16 step.
-__device__ __forceinline__ void gemm_stage(GemmCore &c, uint16_t *xs, const uint16_t *xs_lane, const WRegs &wc,
-                                           WRegs &wn, XRegs &x, const WFrag (&wf)[kFrags], uint32_t K,
-                                           uint32_t group, __amdgpu_buffer_rsrc_t xr, bool x_ok, uint32_t xsrc,
-                                           uint32_t s, uint32_t stages, uint32_t xrow, uint32_t xhalf, uint32_t half,
-                                           const bool (&slab)[4]) {
-  __syncthreads();  // every wave is done reading the previous activation tile
-#pragma unroll
-  for (int j = 0; j < 8; ++j) *reinterpret_cast<uint4 *>(xs + xs_off(xrow, 8u * xhalf + j)) = x.x[j];
-  __syncthreads();
-  if (s + 1 < stages) {
-    load_w(wn, wf, K, group, (s + 1) * kKS + 64u * half);
-    load_x(x, xr, x_ok, xsrc, K, (s + 1) * kKS + 64u * xhalf);
-  }
-  float sf[kFrags][2], bf[kFrags][2];
-#pragma unroll
-  for (uint32_t f = 0; f < kFrags; ++f)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      sf[f][h] = bf16_to_f32(wc.s[f][h]);
-      bf[f][h] = bf16_to_f32(wc.b[f][h]);
-    }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {  // k16 steps: inputs k0 + 64 half + 8 j
-    bf16x8_t b[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) b[t] = *reinterpret_cast<const bf16x8_t *>(xs_lane + 32u * t * kXRow + 8u * j);
-#pragma unroll
-    for (uint32_t f = 0; f < kFrags; ++f) {
-      const uint4 &q = wc.w[f][j >> 2];
-      const uint32_t word = (j & 3) == 0 ? q.x : (j & 3) == 1 ? q.y : (j & 3) == 2 ? q.z : q.w;
-      const bf16x8_t a = dequant_word(word, sf[f][j >> 2], bf[f][j >> 2]);
-#pragma unroll
-      for (int t = 0; t < 4; ++t)
-        if (slab[t]) c.acc[f][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b[t], c.acc[f][t], 0, 0, 0);
-    }
+template <int G>
+__device__ __forceinline__ void load_wstage(WStage &r, const WRow &wr, uint32_t K, uint32_t stage, uint32_t half) {
+  const uint32_t k0 = stage * kKS + 64u * half;
+  const uint32_t off_w = wr.ok ? wr.row * (K / 2u) + k0 / 2u : kOutOfRange;
+  const uint32_t off_g = wr.ok ? (wr.row * (K / G) + k0 / G) * 2u : kOutOfRange;
+  r.w[0] = buf_load16(wr.e.w, off_w);
+  r.w[1] = buf_load16(wr.e.w, off_w + 16u);
+  if constexpr (G == 32) {
+    r.s = buf_load4(wr.e.s, off_g);
+    r.b = buf_load4(wr.e.b, off_g);
+  } else {
+    r.s = buf_load2(wr.e.s, off_g);
+    r.b = buf_load2(wr.e.b, off_g);
   }
 }
 
-__device__ __forceinline__ void gemm_core(GemmCore &c, uint16_t *xs, const WFrag (&wf)[kFrags], uint32_t K,
-                                          uint32_t group, __amdgpu_buffer_rsrc_t xr, bool x_ok, uint32_t xsrc,
-                                          uint32_t count) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const uint32_t half = static_cast<uint32_t>(lane) >> 5;
-  const uint32_t xrow = static_cast<uint32_t>(tid) >> 1, xhalf = static_cast<uint32_t>(tid) & 1u;
+// A thread's share of the activation tile of one stage: kXChunks 16-byte
+// chunks (32 inputs) of tile row tid / kXParts, part tid % kXParts.
+struct XStage {
+  uint4 x[kXChunks];
+};
+
+__device__ __forceinline__ void load_xstage(XStage &r, __amdgpu_buffer_rsrc_t xr, uint32_t src, uint32_t K,
+                                            uint32_t stage, uint32_t xpart) {
+  const uint32_t off = src != ~0u ? (src * K + stage * kKS + 8u * kXChunks * xpart) * 2u : kOutOfRange;
 #pragma unroll
-  for (uint32_t f = 0; f < kFrags; ++f)
+  for (uint32_t j = 0; j < kXChunks; ++j) r.x[j] = buf_load16(xr, off + 16u * j);
+}
+
+__device__ __forceinline__ void store_xstage(uint16_t *xb, const XStage &r, uint32_t xrow, uint32_t xpart) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+  for (uint32_t j = 0; j < kXChunks; ++j)
+    *reinterpret_cast<uint4 *>(xb + xs_off(xrow, kXChunks * xpart + j)) = r.x[j];
+}
+
+// One k16 step: C[32 weight rows x 32 tile rows] += A . B for the NSLAB
+// active slabs (the tile's rows, 32 per slab), with `xl` the lane's base in
+// the LDS activation tile (row lane%32, inputs 64 h) and j the step within
+// the stage.  The slab count is a template argument so that no branch splits
+// the MFMA stream.
+template <int NSLAB>
+__device__ __forceinline__ void mma_step(f32x16_t (&acc)[4], const uint16_t *xl, const bf16x8_t &a, int j) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) c.acc[f][j][r] = 0.0f;
-  bool slab[4];
+  for (int t = 0; t < NSLAB; ++t) {
+    const bf16x8_t b = *reinterpret_cast<const bf16x8_t *>(xl + 32u * t * kXRow + 8u * j);
+    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[t], 0, 0, 0);
+  }
+}
+
+// A stage of MFMAs from ring slot `w`, refilling the slot for the load
+// cursor's stage as soon as each part of it has been consumed (scales and
+// biases first, then the first and second four words), so that a slot's
+// registers are never live twice.
+template <int G, int NSLAB>
+__device__ __forceinline__ void stage_mma(f32x16_t (&acc)[4], const uint16_t *xl, WStage &w, const WRow &lw,
+                                          uint32_t K, uint32_t ls, uint32_t half) {
+  const float s0 = __uint_as_float(w.s << 16), b0 = __uint_as_float(w.b << 16);
+  const float s1 = G == 32 ? __uint_as_float(w.s & 0xffff0000u) : s0;
+  const float b1 = G == 32 ? __uint_as_float(w.b & 0xffff0000u) : b0;
+  const uint32_t k0 = ls * kKS + 64u * half;
+  const uint32_t off_w = lw.ok ? lw.row * (K / 2u) + k0 / 2u : kOutOfRange;
+  const uint32_t off_g = lw.ok ? (lw.row * (K / G) + k0 / G) * 2u : kOutOfRange;
+  if constexpr (G == 32) {
+    w.s = buf_load4(lw.e.s, off_g);
+    w.b = buf_load4(lw.e.b, off_g);
+  } else {
+    w.s = buf_load2(lw.e.s, off_g);
+    w.b = buf_load2(lw.e.b, off_g);
+  }
+  // Software pipeline over the eight k16 steps: the A operand of step j+1 is
+  // dequantized while the MFMAs of step j run; a scheduling barrier per step
+  // keeps the compiler from hoisting further ahead (which only adds live
+  // registers: the other wave on the SIMD covers the LDS latency).
+  bf16x8_t a = dequant_word(w.w[0].x, s0, b0);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) slab[j] = 32u * j < count;
-  const uint32_t stages = K / kKS;
-  WRegs w0, w1;
-  XRegs x;
-  load_w(w0, wf, K, group, 64u * half);
-  load_x(x, xr, x_ok, xsrc, K, 64u * xhalf);
-  const uint16_t *xs_lane = xs + (lane & 31) * kXRow + 64u * half;
-  // Two stages per trip so the weight registers alternate without copies.
-  for (uint32_t s = 0; s < stages; s += 2) {
-    gemm_stage(c, xs, xs_lane, w0, w1, x, wf, K, group, xr, x_ok, xsrc, s, stages, xrow, xhalf, half, slab);
-    if (s + 1 < stages)
-      gemm_stage(c, xs, xs_lane, w1, w0, x, wf, K, group, xr, x_ok, xsrc, s + 1, stages, xrow, xhalf, half, slab);
+  for (int j = 0; j < 8; ++j) {
+    bf16x8_t an = a;
+    if (j < 7) {
+      const int k = j + 1;
+      const uint4 &q = w.w[k >> 2];
+      const uint32_t word = (k & 3) == 0 ? q.x : (k & 3) == 1 ? q.y : (k & 3) == 2 ? q.z : q.w;
+      an = dequant_word(word, k < 4 ? s0 : s1, k < 4 ? b0 : b1);
+    }
+    if (j == 3) w.w[0] = buf_load16(lw.e.w, off_w);  // words 0-3 consumed
+    if (j == 7) w.w[1] = buf_load16(lw.e.w, off_w + 16u);
+    mma_step<NSLAB>(acc, xl, a, j);
+    a = an;
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -399,149 +390,293 @@ struct XcdItems {
   __device__ __forceinline__ uint32_t tile(uint32_t j) const { return xcd + 8u * (j / nb_count); }
 };
 
-struct GateUpParams {
-  const uint16_t *x;
-  uint32_t tokens;
-  MqProjection gate, up;
-  MqProjection sgate, sup;  // shared expert (dense, expert 0) or unused
+struct GemmParams {
+  const uint16_t *x;     // gate/up: token activations [tokens, K]; down: act [rows, K] in sorted order
+  uint32_t x_bytes;
+  MqProjection w0, w1;   // gate/up: gate, up; down: down (w1 unused)
+  MqProjection s0, s1;   // the shared expert's matching projections (dense, expert 0) or unused
   const GroupTile *tiles;
+  uint32_t tiles_bytes;
   const uint32_t *n_tiles;
   const uint32_t *order;
-  uint16_t *act;  // [rows, inter] sorted order
-  uint32_t slots, routed_rows, hidden, inter, group, dense_count;
+  uint32_t order_bytes;
+  uint16_t *out;         // gate/up: act [rows, N] sorted; down: y [routed_rows, N]
+  uint16_t *out_shared;  // down: the shared expert's output [tokens, N] or null
+  uint32_t slots, routed_rows, K, N, dense_count;
   unsigned int *err;
 };
 
-// Fragment F (0..7) of a gate/up block holds gate features 16 F .. +15 in
-// its rows 0-15 and the matching up features in rows 16-31, so a lane's C
-// registers r and r+8 are gate and up of the same feature.
-__global__ __launch_bounds__(256, 2) void grouped_gateup_kernel(GateUpParams p) {
-  __shared__ __align__(16) uint16_t xs[kTileRows * kXRow];
-  __shared__ uint32_t row_src[kTileRows];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const uint32_t wave = wave_id();
-  const uint32_t nb_count = (p.inter + kGateUpFeatures - 1) / kGateUpFeatures;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.tokens * p.hidden * 2u);
-  const XcdItems it(*p.n_tiles, nb_count);
-  for (uint32_t j = it.first; j < it.count; j += it.stride) {
-    const uint32_t nb = j % nb_count;
-    const GroupTile tile = p.tiles[it.tile(j)];
-    __syncthreads();  // the previous item is done with row_src
-    if (tid < static_cast<int>(kTileRows)) {
-      uint32_t src = ~0u;
-      if (static_cast<uint32_t>(tid) < tile.count) {
-        const uint32_t r = p.order[tile.start + tid];
-        src = r < p.routed_rows ? r / p.slots : r - p.routed_rows;
-      }
-      row_src[tid] = src;
-    }
-    ExpertPtrs eg, eu;
-    if (tile.word == kSharedWord) {
-      eg = expert_ptrs(p.sgate, 0u, p.inter, p.hidden, p.group, 1u);
-      eu = expert_ptrs(p.sup, 0u, p.inter, p.hidden, p.group, 1u);
-    } else {
-      eg = expert_ptrs(p.gate, tile.word, p.inter, p.hidden, p.group, p.dense_count);
-      eu = expert_ptrs(p.up, tile.word, p.inter, p.hidden, p.group, p.dense_count);
-    }
-    if ((!eg.ok || !eu.ok) && tid == 0 && tile.word != kDeadWord) raise_flag(p.err, MQ_DEVFLAG_BAD_ROUTE);
-    __syncthreads();
-    // Lane rows: fragment row (lane % 32) < 16 is a gate row, else an up row.
-    const bool up_half = (lane & 31) >= 16;
-    const ExpertRsrc rg = expert_rsrc(eg, p.inter, p.hidden, p.group);
-    const ExpertRsrc ru = expert_rsrc(eu, p.inter, p.hidden, p.group);
-    WFrag wf[kFrags];
-#pragma unroll
-    for (uint32_t f = 0; f < kFrags; ++f) {
-      const uint32_t frag = wave * kFrags + f;
-      const uint32_t feature = nb * kGateUpFeatures + 16u * frag + (lane & 15);
-      wf[f] = {up_half ? ru : rg, feature, feature < p.inter};
-    }
-    const uint32_t xsrc = row_src[static_cast<uint32_t>(tid) >> 1];
-    GemmCore c;
-    gemm_core(c, xs, wf, p.hidden, p.group, xr, xsrc != ~0u, xsrc, tile.count);
-    // Epilogue: act = swiglu(bf16(g), bf16(u)) in sorted row order.
+// A work item of the block's sequence, as fetched ahead of use.  The fields
+// loaded from memory stay in vector registers and are made uniform only where
+// used, so that issuing the fetch never waits for it.
+struct Item {
+  uint32_t j;       // index in the XCD's item list (uniform)
+  uint4 tile;       // GroupTile: word, start, count (all zero past the end)
+  uint32_t xraw;    // gate/up: `order` entry of this thread's tile row
+  uint32_t dst[4];  // down: `order` entries of this lane's tile rows in the four slabs
+};
+
+__device__ __forceinline__ void fetch_tile(Item &m, uint32_t j, const XcdItems &it, __amdgpu_buffer_rsrc_t tr) {
+  m.j = j;
+  m.tile = buf_load16(tr, j < it.count ? it.tile(j) * 16u : kOutOfRange);
+}
+
+// Second fetch step, once the tile record has arrived: the sorted-row entries.
+template <bool DOWN>
+__device__ __forceinline__ void fetch_rows(Item &m, __amdgpu_buffer_rsrc_t orr, int tid) {
+  const uint32_t start = m.tile.y, count = m.tile.z;
+  if constexpr (DOWN) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const uint32_t trow = 32u * t + (lane & 31);
-      if (trow >= tile.count) continue;
-      uint16_t *dst = p.act + static_cast<uint64_t>(tile.start + trow) * p.inter;
+      const uint32_t i = 32u * t + (static_cast<uint32_t>(tid) & 31u);
+      m.dst[t] = buf_load4(orr, i < count ? (start + i) * 4u : kOutOfRange);
+    }
+  } else {
+    const uint32_t i = static_cast<uint32_t>(tid) / kXParts;
+    m.xraw = buf_load4(orr, i < count ? (start + i) * 4u : kOutOfRange);
+  }
+}
+
+// This thread's activation row for the item's X loads (~0u: none).
+template <bool DOWN>
+__device__ __forceinline__ uint32_t x_source(const Item &m, const GemmParams &p, int tid) {
+  const uint32_t i = static_cast<uint32_t>(tid) / kXParts;
+  if (i >= m.tile.z) return ~0u;
+  if constexpr (DOWN) return m.tile.y + i;
+  else return m.xraw < p.routed_rows ? m.xraw / p.slots : m.xraw - p.routed_rows;
+}
+
+// The lane's weight row of an item.  Gate/up: waves 0-3 stream gate rows and
+// waves 4-7 the up rows of the same 128 features; down: wave w streams rows
+// 32 w .. +31 of the item's 256 output features.
+template <bool DOWN, int G>
+__device__ __forceinline__ WRow weight_row(const Item &m, const GemmParams &p, const XcdItems &it,
+                                           uint32_t nb_count, uint32_t wave, int lane) {
+  const bool valid = m.j < it.count;
+  const uint32_t word = uniform(m.tile.x);
+  const uint32_t nb = m.j % nb_count;
+  const bool shared = word == kSharedWord;
+  ExpertPtrs e;
+  uint32_t row;
+  if constexpr (DOWN) {
+    if (shared) e = expert_ptrs(p.s0, 0u, p.N, p.K, G, 1u);
+    else e = expert_ptrs(p.w0, word, p.N, p.K, G, p.dense_count);
+    row = nb * kDownFeatures + 32u * wave + (static_cast<uint32_t>(lane) & 31u);
+  } else {
+    if (wave < kGemmWaves / 2) {
+      if (shared) e = expert_ptrs(p.s0, 0u, p.N, p.K, G, 1u);
+      else e = expert_ptrs(p.w0, word, p.N, p.K, G, p.dense_count);
+    } else {
+      if (shared) e = expert_ptrs(p.s1, 0u, p.N, p.K, G, 1u);
+      else e = expert_ptrs(p.w1, word, p.N, p.K, G, p.dense_count);
+    }
+    row = nb * kGateUpFeatures + 32u * (wave % (kGemmWaves / 2)) + (static_cast<uint32_t>(lane) & 31u);
+  }
+  if (valid && !e.ok && word != kDeadWord && lane == 0) raise_flag(p.err, MQ_DEVFLAG_BAD_ROUTE);
+  WRow r;
+  r.e = expert_rsrc(e, p.N, p.K, G);
+  r.row = row;
+  r.ok = valid && e.ok && row < p.N;
+  return r;
+}
+
+// Gate/up epilogue: act = swiglu(bf16(g), bf16(u)) in sorted row order.  The
+// up waves hand their bf16 results to the gate waves through LDS (the tile
+// buffer just consumed); lane l of up wave 4+f holds exactly the (row,
+// feature) cells of lane l of gate wave f.
+constexpr uint32_t kExchange = 4u * 4u * 64u * 4u;  // bf16 per gate/up wave pair: 4 slabs x 16 values x 64 lanes
+static_assert(kExchange * (kGemmWaves / 2) <= kXTile, "gate/up exchange must fit in one activation tile");
+
+__device__ __forceinline__ void gateup_epilogue(const f32x16_t (&acc)[4], uint16_t *xb, const Item &m,
+                                                const GemmParams &p, uint32_t nb, uint32_t wave, int lane,
+                                                const bool (&slab)[4]) {
+  const uint32_t fw = wave % (kGemmWaves / 2);
+  uint16_t *ex = xb + fw * kExchange;
+  __syncthreads();  // every wave is done reading the tile in xb
+  if (wave >= kGemmWaves / 2) {
 #pragma unroll
-      for (uint32_t f = 0; f < kFrags; ++f) {
-        const uint32_t frag = wave * kFrags + f;
+    for (int t = 0; t < 4; ++t)
+      if (slab[t])
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          const uint32_t feat = nb * kGateUpFeatures + 16u * frag + c_row(r, lane);
-          if (feat >= p.inter) continue;
-          const float g = round_bf16(c.acc[f][t][r]);
-          const float u = round_bf16(c.acc[f][t][r + 8]);
-          dst[feat] = f32_to_bf16(swiglu_bf16(g, u));
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<uint2 *>(ex + ((4u * t + q) * 64u + lane) * 4u) =
+              make_uint2(pack_bf16(acc[t][4 * q], acc[t][4 * q + 1]), pack_bf16(acc[t][4 * q + 2], acc[t][4 * q + 3]));
+  }
+  __syncthreads();
+  if (wave < kGemmWaves / 2) {
+    const uint32_t start = uniform(m.tile.y), count = uniform(m.tile.z);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t trow = 32u * t + (static_cast<uint32_t>(lane) & 31u);
+      if (!slab[t] || trow >= count) continue;
+      uint16_t *dst = p.out + static_cast<uint64_t>(start + trow) * p.N;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {  // four runs of 4 consecutive features
+        const uint32_t feat = nb * kGateUpFeatures + 32u * fw + c_row(4 * q, lane);
+        const uint2 u = *reinterpret_cast<const uint2 *>(ex + ((4u * t + q) * 64u + lane) * 4u);
+        const uint32_t uu[2] = {u.x, u.y};
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float g = round_bf16(acc[t][4 * q + e]);
+          const float up = __uint_as_float((e & 1) ? (uu[e >> 1] & 0xffff0000u) : (uu[e >> 1] << 16));
+          v[e] = swiglu_bf16(g, up);
         }
+        if (feat < p.N) *reinterpret_cast<uint2 *>(dst + feat) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
       }
     }
   }
 }
 
-struct DownParams {
-  const uint16_t *act;
-  uint32_t rows;
-  MqProjection down, sdown;
-  const GroupTile *tiles;
-  const uint32_t *n_tiles;
-  const uint32_t *order;
-  uint16_t *y;         // [routed_rows, hidden]
-  uint16_t *y_shared;  // [tokens, hidden] or null
-  uint32_t routed_rows, hidden, inter, group, dense_count;
+// Down epilogue: the bf16 outputs go back to y[token, slot] (or the shared
+// expert's row).
+__device__ __forceinline__ void down_epilogue(const f32x16_t (&acc)[4], const Item &m, const GemmParams &p,
+                                              uint32_t nb, uint32_t wave, int lane, const bool (&slab)[4]) {
+  const uint32_t count = uniform(m.tile.z);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t trow = 32u * t + (static_cast<uint32_t>(lane) & 31u);
+    if (!slab[t] || trow >= count) continue;
+    const uint32_t r = m.dst[t];
+    uint16_t *dst = r < p.routed_rows ? p.out + static_cast<uint64_t>(r) * p.N
+                                      : p.out_shared + static_cast<uint64_t>(r - p.routed_rows) * p.N;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t feat = nb * kDownFeatures + 32u * wave + c_row(4 * q, lane);
+      if (feat < p.N)
+        *reinterpret_cast<uint2 *>(dst + feat) =
+            make_uint2(pack_bf16(acc[t][4 * q], acc[t][4 * q + 1]), pack_bf16(acc[t][4 * q + 2], acc[t][4 * q + 3]));
+    }
+  }
+}
+
+// Pipeline state carried across stages and items: the weight ring, the load
+// cursor (row and stage, NS stages ahead of compute), and the activation
+// registers of the next stage with their source rows.
+template <bool DOWN, int NS, int G>
+struct Pipe {
+  WStage ring[NS];
+  WRow lw;
+  uint32_t ls;
+  XStage xv;
+  uint32_t xsrc, xsrc_next;
+
+  // All stages of one item with NSLAB active slabs.  NS divides S, so ring
+  // slot u always holds stage s0 + u and the item ends with an unrolled trip.
+  template <int NSLAB>
+  __device__ __forceinline__ void run(f32x16_t (&acc)[4], uint16_t *xs, const Item &n, const Item &n2,
+                                      const GemmParams &p, const XcdItems &it, uint32_t nb_count, uint32_t wave,
+                                      int lane, int tid, uint32_t S, __amdgpu_buffer_rsrc_t xr) {
+    const uint32_t half = static_cast<uint32_t>(lane) >> 5;
+    const uint32_t xrow = static_cast<uint32_t>(tid) / kXParts, xpart = static_cast<uint32_t>(tid) % kXParts;
+    const uint32_t xl_off = (static_cast<uint32_t>(lane) & 31u) * kXRow + 64u * half;
+    for (uint32_t s0 = 0; s0 < S; s0 += NS) {
+#pragma unroll
+      for (int u = 0; u < NS; ++u) {
+        const uint32_t s = s0 + u;
+        uint16_t *xb = xs + (s & 1u) * kXTile;
+        store_xstage(xb, xv, xrow, xpart);
+        __syncthreads();
+        const bool last = u == NS - 1 && s + 1u == S;
+        if (last) xsrc_next = x_source<DOWN>(n, p, tid);
+        load_xstage(xv, xr, last ? xsrc_next : xsrc, p.K, last ? 0u : s + 1u, xpart);
+        stage_mma<G, NSLAB>(acc, xb + xl_off, ring[u], lw, p.K, ls, half);
+        if (++ls == S) {
+          // The load cursor finished an item.  With NS == S it was already
+          // in the next item n, and this is compute's last stage of c.
+          ls = 0;
+          lw = weight_row<DOWN, G>(last ? n2 : n, p, it, nb_count, wave, lane);
+        }
+      }
+    }
+  }
 };
 
-// Fragment F (0..7) of a down block holds features 32 F .. +31.
-__global__ __launch_bounds__(256, 2) void grouped_down_kernel(DownParams p) {
-  __shared__ __align__(16) uint16_t xs[kTileRows * kXRow];
-  __shared__ uint32_t row_dst[kTileRows];
+// The grouped GEMM, persistent over the block's work items (tile, feature
+// block).  Per stage of kKS inputs: the activations loaded one stage earlier
+// go to one of two LDS tiles (one barrier per stage), the next stage's
+// activations and the weights NS stages ahead are issued, and the stage's
+// weights (loaded NS stages earlier into ring slot u) are dequantized and fed
+// to the MFMAs.  The stage sequence runs on across items: the weight loads of
+// the next item start while the current one finishes (NS <= stages per item,
+// so the load cursor is at most one item ahead), and tile records and sorted
+// rows are fetched two items ahead.
+template <bool DOWN, int NS, int G>
+__global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmParams p) {
+  __shared__ __align__(16) uint16_t xs[2 * kXTile];
+  constexpr uint32_t kFeat = DOWN ? kDownFeatures : kGateUpFeatures;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const uint32_t wave = wave_id();
-  const uint32_t nb_count = (p.hidden + kDownFeatures - 1) / kDownFeatures;
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.act, p.rows * p.inter * 2u);
+  const uint32_t half = static_cast<uint32_t>(lane) >> 5;
+  const uint32_t xpart = static_cast<uint32_t>(tid) % kXParts;
+  const uint32_t S = p.K / kKS;
+  const uint32_t nb_count = (p.N + kFeat - 1) / kFeat;
   const XcdItems it(*p.n_tiles, nb_count);
-  for (uint32_t j = it.first; j < it.count; j += it.stride) {
-    const uint32_t nb = j % nb_count;
-    const GroupTile tile = p.tiles[it.tile(j)];
-    __syncthreads();  // the previous item's epilogue is done with row_dst
-    if (tid < static_cast<int>(kTileRows))
-      row_dst[tid] = static_cast<uint32_t>(tid) < tile.count ? p.order[tile.start + tid] : ~0u;
-    const ExpertPtrs ed = tile.word == kSharedWord
-                              ? expert_ptrs(p.sdown, 0u, p.hidden, p.inter, p.group, 1u)
-                              : expert_ptrs(p.down, tile.word, p.hidden, p.inter, p.group, p.dense_count);
-    __syncthreads();
-    const ExpertRsrc e = expert_rsrc(ed, p.hidden, p.inter, p.group);
-    WFrag wf[kFrags];
+  if (it.first >= it.count) return;  // uniform: no work for this block
+  const __amdgpu_buffer_rsrc_t tr = make_rsrc(p.tiles, p.tiles_bytes);
+  const __amdgpu_buffer_rsrc_t orr = make_rsrc(p.order, p.order_bytes);
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+
+  Item c, n, n2;  // the compute item and the next two
+  fetch_tile(c, it.first, it, tr);
+  fetch_tile(n, it.first + it.stride, it, tr);
+  fetch_tile(n2, it.first + 2u * it.stride, it, tr);
+  fetch_rows<DOWN>(c, orr, tid);
+  fetch_rows<DOWN>(n, orr, tid);
+
+  // Load cursor: NS stages ahead of the compute cursor.
+  Pipe<DOWN, NS, G> pp;
+  pp.lw = weight_row<DOWN, G>(c, p, it, nb_count, wave, lane);
+  pp.ls = 0;
 #pragma unroll
-    for (uint32_t f = 0; f < kFrags; ++f) {
-      const uint32_t feature = nb * kDownFeatures + 32u * (wave * kFrags + f) + (lane & 31);
-      wf[f] = {e, feature, feature < p.hidden};
+  for (int u = 0; u < NS; ++u) {
+    load_wstage<G>(pp.ring[u], pp.lw, p.K, pp.ls, half);
+    if (++pp.ls == S) {
+      pp.ls = 0;
+      pp.lw = weight_row<DOWN, G>(n, p, it, nb_count, wave, lane);
     }
-    const uint32_t xrow = static_cast<uint32_t>(tid) >> 1;
-    GemmCore c;
-    gemm_core(c, xs, wf, p.inter, p.group, xr, xrow < tile.count, tile.start + xrow, tile.count);
+  }
+  pp.xsrc = x_source<DOWN>(c, p, tid);
+  pp.xsrc_next = ~0u;
+  load_xstage(pp.xv, xr, pp.xsrc, p.K, 0u, xpart);
+
+  f32x16_t acc[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint32_t trow = 32u * t + (lane & 31);
-      if (trow >= tile.count) continue;
-      const uint32_t r = row_dst[trow];
-      uint16_t *dst = r < p.routed_rows ? p.y + static_cast<uint64_t>(r) * p.hidden
-                                        : p.y_shared + static_cast<uint64_t>(r - p.routed_rows) * p.hidden;
+  for (int t = 0; t < 4; ++t)
 #pragma unroll
-      for (uint32_t f = 0; f < kFrags; ++f)
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+  bool slab[4];
+  uint32_t count = uniform(c.tile.z);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {  // four runs of 4 consecutive features
-          const uint32_t feat = nb * kDownFeatures + 32u * (wave * kFrags + f) + c_row(4 * q, lane);
-          if (feat >= p.hidden) continue;
-          const uint32_t lo = pack_bf16(c.acc[f][t][4 * q], c.acc[f][t][4 * q + 1]);
-          const uint32_t hi = pack_bf16(c.acc[f][t][4 * q + 2], c.acc[f][t][4 * q + 3]);
-          *reinterpret_cast<uint2 *>(dst + feat) = make_uint2(lo, hi);
-        }
+  for (int t = 0; t < 4; ++t) slab[t] = 32u * t < count;
+  uint32_t nb = c.j % nb_count;
+  for (;;) {
+    switch ((count + 31u) / 32u) {  // active slabs (uniform)
+      case 0:
+      case 1: pp.template run<1>(acc, xs, n, n2, p, it, nb_count, wave, lane, tid, S, xr); break;
+      case 2: pp.template run<2>(acc, xs, n, n2, p, it, nb_count, wave, lane, tid, S, xr); break;
+      case 3: pp.template run<3>(acc, xs, n, n2, p, it, nb_count, wave, lane, tid, S, xr); break;
+      default: pp.template run<4>(acc, xs, n, n2, p, it, nb_count, wave, lane, tid, S, xr); break;
     }
+    // Every item starts on LDS tile 0; its last stage used tile (S - 1) & 1.
+    if constexpr (DOWN) down_epilogue(acc, c, p, nb, wave, lane, slab);
+    else gateup_epilogue(acc, xs + ((S - 1u) & 1u) * kXTile, c, p, nb, wave, lane, slab);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+    c = n;
+    n = n2;
+    fetch_tile(n2, c.j + 2u * it.stride, it, tr);
+    fetch_rows<DOWN>(n, orr, tid);
+    pp.xsrc = pp.xsrc_next;
+    if (c.j >= it.count) break;  // uniform
+    count = uniform(c.tile.z);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) slab[t] = 32u * t < count;
+    nb = c.j % nb_count;
+    if (S & 1u) __syncthreads();  // odd S: tile 0 is reused back to back across the item boundary
   }
 }
 
@@ -609,6 +744,28 @@ int validate_proj_grouped(const MqProjection &p, const char *name) {
   if ((p.pool != nullptr || p.stream_pack != nullptr) && p.pool_stride == 0)
     return fail(MQ_ERR_INVALID, "%s projection record stride is zero", name);
   return MQ_OK;
+}
+
+// Weight stages in flight: a divisor of the stages per item (3..5 where one
+// divides it), so the ring slot of a stage is fixed and the load cursor
+// stays within one item of the compute cursor.
+template <bool DOWN, int NS>
+int launch_gemm_ns(const GemmParams &p, uint32_t group, uint32_t grid, hipStream_t s) {
+  if (group == 32)
+    hipLaunchKernelGGL((grouped_gemm_kernel<DOWN, NS, 32>), dim3(grid), dim3(kGemmThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((grouped_gemm_kernel<DOWN, NS, 64>), dim3(grid), dim3(kGemmThreads), 0, s, p);
+  return check_launch(DOWN ? "grouped_gemm_kernel (down)" : "grouped_gemm_kernel (gate/up)");
+}
+
+template <bool DOWN>
+int launch_gemm(const GemmParams &p, uint32_t group, uint32_t grid, hipStream_t s) {
+  const uint32_t stages = p.K / kKS;
+  if (stages % 4 == 0) return launch_gemm_ns<DOWN, 4>(p, group, grid, s);
+  if (stages % 5 == 0) return launch_gemm_ns<DOWN, 5>(p, group, grid, s);
+  if (stages % 3 == 0) return launch_gemm_ns<DOWN, 3>(p, group, grid, s);
+  if (stages % 2 == 0) return launch_gemm_ns<DOWN, 2>(p, group, grid, s);
+  return launch_gemm_ns<DOWN, 1>(p, group, grid, s);
 }
 
 KeySpace key_space(const MqGroupedArgs &a) {
@@ -688,51 +845,46 @@ extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
   int device = 0, cus = 0;
   MQ_TRY_HIP(hipGetDevice(&device));
   MQ_TRY_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
-  // One 256-thread block per CU, a multiple of 8 (XCD-aware item schedule).
-  const uint32_t resident = std::max(8u, (static_cast<uint32_t>(cus > 0 ? cus : 256) * 2u / 8u) * 8u);
+  // One 8-wave block per CU, a multiple of 8 (XCD-aware item schedule).
+  const uint32_t resident = std::max(8u, (static_cast<uint32_t>(cus > 0 ? cus : 256) / 8u) * 8u);
 
-  GateUpParams gp{};
+  GemmParams gp{};
   gp.x = a.x;
-  gp.tokens = a.tokens;
-  gp.gate = a.gate;
-  gp.up = a.up;
+  gp.x_bytes = a.tokens * a.hidden * 2u;
+  gp.w0 = a.gate;
+  gp.w1 = a.up;
   if (shared_expert) {
-    gp.sgate = a.shared_expert[0];
-    gp.sup = a.shared_expert[1];
+    gp.s0 = a.shared_expert[0];
+    gp.s1 = a.shared_expert[1];
   }
   gp.tiles = tiles;
+  gp.tiles_bytes = l.max_tiles * static_cast<uint32_t>(sizeof(GroupTile));
   gp.n_tiles = n_tiles;
   gp.order = order;
-  gp.act = act;
+  gp.order_bytes = l.rows * 4u;
+  gp.out = act;
   gp.slots = a.slots;
   gp.routed_rows = routed_rows;
-  gp.hidden = a.hidden;
-  gp.inter = a.inter;
-  gp.group = a.group_size;
+  gp.K = a.hidden;
+  gp.N = a.inter;
   gp.dense_count = a.expert_count;
   gp.err = err;
   const uint32_t gu_items = l.max_tiles * ceil_div(a.inter, kGateUpFeatures);
-  hipLaunchKernelGGL(grouped_gateup_kernel, dim3(std::min(ceil_div(gu_items, 8) * 8u, resident)), dim3(256), 0, s, gp);
-  if ((rc = check_launch("grouped_gateup_kernel"))) return rc;
+  if ((rc = launch_gemm<false>(gp, a.group_size, std::min(ceil_div(gu_items, 8) * 8u, resident), s))) return rc;
 
-  DownParams dp{};
-  dp.act = act;
-  dp.rows = l.rows;
-  dp.down = a.down;
-  if (shared_expert) dp.sdown = a.shared_expert[2];
-  dp.tiles = tiles;
-  dp.n_tiles = n_tiles;
-  dp.order = order;
-  dp.y = a.y;
-  dp.y_shared = y_shared;
-  dp.routed_rows = routed_rows;
-  dp.hidden = a.hidden;
-  dp.inter = a.inter;
-  dp.group = a.group_size;
-  dp.dense_count = a.expert_count;
+  GemmParams dp = gp;
+  dp.x = act;
+  dp.x_bytes = l.rows * a.inter * 2u;
+  dp.w0 = a.down;
+  dp.w1 = MqProjection{};
+  dp.s0 = shared_expert ? a.shared_expert[2] : MqProjection{};
+  dp.s1 = MqProjection{};
+  dp.out = a.y;
+  dp.out_shared = y_shared;
+  dp.K = a.inter;
+  dp.N = a.hidden;
   const uint32_t dn_items = l.max_tiles * ceil_div(a.hidden, kDownFeatures);
-  hipLaunchKernelGGL(grouped_down_kernel, dim3(std::min(ceil_div(dn_items, 8) * 8u, resident)), dim3(256), 0, s, dp);
-  if ((rc = check_launch("grouped_down_kernel"))) return rc;
+  if ((rc = launch_gemm<true>(dp, a.group_size, std::min(ceil_div(dn_items, 8) * 8u, resident), s))) return rc;
 
   if (a.out != nullptr) {
     const uint16_t *shared_vec = shared_expert ? y_shared : a.shared;

@@ -271,6 +271,10 @@ __device__ __forceinline__ uint16_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t
   return __builtin_amdgcn_raw_buffer_load_b16(r, static_cast<int>(off), 0, 0);
 }
 
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0));
+}
+
 // Descriptors of one projection of one expert (size 0 when the word is invalid).
 struct ExpertRsrc {
   __amdgpu_buffer_rsrc_t w, s, b;

@@ -48,7 +48,9 @@ class DecodeLayer:
     """One MoE decode layer for a fixed token count, with preallocated buffers."""
 
     def __init__(self, weights: LayerWeights, tokens: int, top_k: int, *, threshold: float = 1.0,
-                 min_keep: int = 1, blend: float = 1.0, device="cuda"):
+                 min_keep: int = 1, blend: float = 1.0, device="cuda", x: torch.Tensor | None = None):
+        """``x``: optional caller-owned bf16 ``[tokens, hidden]`` input buffer
+        (e.g. a row of a larger staging tensor); allocated here when omitted."""
         lay = weights.layout
         self.w = weights
         self.tokens, self.top_k = tokens, top_k
@@ -56,7 +58,11 @@ class DecodeLayer:
         self.experts = weights.router_w.shape[0]
         dev = torch.device(device)
         bf = torch.bfloat16
-        self.x = torch.zeros((tokens, self.hidden), dtype=bf, device=dev)
+        if x is None:
+            x = torch.zeros((tokens, self.hidden), dtype=bf, device=dev)
+        elif x.dtype != bf or tuple(x.shape) != (tokens, self.hidden) or not x.is_contiguous() or x.device != dev:
+            raise ValueError(f"x must be a contiguous bf16 [{tokens}, {self.hidden}] tensor on {dev}")
+        self.x = x
         self.logits = torch.empty((tokens, self.experts), dtype=bf, device=dev)
         self.inds = torch.empty((tokens, top_k), dtype=torch.int32, device=dev)
         self.scores = torch.empty((tokens, top_k), dtype=bf, device=dev)
