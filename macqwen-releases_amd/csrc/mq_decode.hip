@@ -422,20 +422,28 @@ __global__ __launch_bounds__(kThreads) void gateup_kernel(
     gv[i] = Sl::reduce(row_partial<TT, CPL>(rg[i], xl));
     uv[i] = Sl::reduce(row_partial<TT, CPL>(ru[i], xl));
   }
-  // Epilogue: one lane per row (lane i of the wave for SW = 64, lane 0 of each
-  // slice for SW = 16), so the double-precision exp runs in parallel.
+  // Epilogue in one pass: lane i takes row i of the wave (SW = 64; the row
+  // sums are wave-uniform) or lane 0 of each slice its slice's row (SW = 16),
+  // so the SwiGLU sequence runs once for all of the wave's rows.
+  float gsel = gv[0], usel = uv[0];
+  uint32_t rsel = row0 + sub;
+  bool mine = li == 0;
+  if constexpr (SW == 64) {
 #pragma unroll
-  for (int i = 0; i < R; ++i) {
-    const bool mine = SW == 64 ? (lane == i) : (li == 0);
-    const uint32_t row = row0 + i * Sl::kRows + sub;
-    if (mine && row < inter) {
-      const float gt = TT::round(gv[i]);
-      const float ut = TT::round(uv[i]);
-      const uint64_t idx = static_cast<uint64_t>(pair) * inter + row;
-      act[idx] = TT::store(swiglu_t<TT>(gt, ut));
-      if (gate_out != nullptr && !is_shared) gate_out[idx] = TT::store(gt);
-      if (up_out != nullptr && !is_shared) up_out[idx] = TT::store(ut);
+    for (int i = 1; i < R; ++i) {
+      gsel = lane == i ? gv[i] : gsel;
+      usel = lane == i ? uv[i] : usel;
     }
+    rsel = row0 + static_cast<uint32_t>(lane) * Sl::kRows;
+    mine = lane < R;
+  }
+  if (mine && rsel < inter) {
+    const float gt = TT::round(gsel);
+    const float ut = TT::round(usel);
+    const uint64_t idx = static_cast<uint64_t>(pair) * inter + rsel;
+    act[idx] = TT::store(swiglu_t<TT>(gt, ut));
+    if (gate_out != nullptr && !is_shared) gate_out[idx] = TT::store(gt);
+    if (up_out != nullptr && !is_shared) up_out[idx] = TT::store(ut);
   }
 }
 
@@ -450,12 +458,16 @@ __global__ void swiglu_kernel(const typename TT::storage *__restrict__ g, const 
 enum SharedMode : int { kSharedNone = 0, kSharedY = 1, kSharedParts = 2, kSharedExpert = 3 };
 
 // Down + score combine + shared epilogue.  A block owns Slice<SW>::kRows
-// output rows of one token; its four waves split the token's active sources
-// (routed slots s < keep, then the shared expert) round-robin, so every wave
-// streams only its sources' weight rows and activation chunks, and the grid
-// has (hidden / kRows) * tokens blocks to spread the weight stream over the
-// whole chip.  Each wave handles its sources in batches of SPW: activations
-// issued first, then the weight rows, then the row dots (independent chains).
+// output rows of one token; its four waves split the token's sources
+// round-robin, so every wave streams only its sources' weight rows and
+// activation chunks, and the grid has (hidden / kRows) * tokens blocks to
+// spread the weight stream over the whole chip.  Source 0 is the in-kernel
+// shared expert (when present), then routed slots 0, 1, ...: a source's
+// activation row does not depend on the keep count, so the activation loads
+// are issued before anything has arrived.  The token's route words, scores
+// and keep count come in one round of loads (lane s holds slot s).  Each wave
+// handles its sources in batches of SPW: activations first, then the weight
+// rows once the route words are in, then the row dots (independent chains).
 // The T-rounded projections d go to LDS and wave 0 combines them in slot
 // order: acc += float(d) * float(score[t,s]) in float32 with no contraction
 // (models/flashnext/metal_runtime.py:291-336), then T(acc) and the shared
@@ -468,7 +480,6 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(
     const uint16_t *__restrict__ shared_gate, typename TT::storage *__restrict__ out, uint32_t tokens,
     uint32_t slots, uint32_t hidden, uint32_t inter, uint32_t group, uint32_t dense_count,
     unsigned int *__restrict__ err) {
-  using S = typename TT::storage;
   using Sl = Slice<SW>;
   constexpr uint32_t kMaxSources = kMaxSlots + 1;
   __shared__ float dsum[kMaxSources][Sl::kRows];
@@ -480,42 +491,53 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(
   const uint32_t token = blockIdx.y;
   const uint32_t row = blockIdx.x * Sl::kRows + sub;
   const bool row_ok = row < hidden;
-  const uint32_t keep = keeps ? min(static_cast<uint32_t>(keeps[token]), slots) : slots;
   const bool with_shared_expert = shared_mode == kSharedExpert;
-  const uint32_t n_act = keep + (with_shared_expert ? 1u : 0u);
+  const uint32_t first_routed = with_shared_expert ? 1u : 0u;  // source index of routed slot 0
+  const uint32_t n_src = slots + first_routed;                // sources before the keep count is known
   const uint32_t routed_pairs = tokens * slots;
   const uint64_t pair0 = static_cast<uint64_t>(token) * slots;
+  const uint32_t ulane = static_cast<uint32_t>(lane);
 
-  // Small per-token inputs, all issued up front (no load waits on another).
-  float score[kMaxSlots];
-#pragma unroll
-  for (uint32_t s = 0; s < kMaxSlots; ++s) {
-    const uint64_t pair = pair0 + min(s, slots - 1u);
-    score[s] = score_dtype == MQ_BF16 ? bf16_to_f32(static_cast<const uint16_t *>(scores)[pair])
-                                      : static_cast<const float *>(scores)[pair];
-  }
+  // One round of small loads: route word and score of slot `lane`, the keep
+  // count, the shared inputs.  Buffer loads with out-of-range offsets for the
+  // unused lanes, so nothing waits on anything else.
+  const uint32_t lane_word =
+      buf_load4(make_rsrc(routes + pair0, slots * 4u), ulane < slots ? ulane * 4u : kOutOfRange);
+  const bool bf16_scores = score_dtype == MQ_BF16;
+  const uint32_t score_bytes = bf16_scores ? 2u : 4u;
+  const __amdgpu_buffer_rsrc_t sr =
+      make_rsrc(static_cast<const uint8_t *>(scores) + pair0 * score_bytes, slots * score_bytes);
+  const uint16_t score16 = buf_load2(sr, bf16_scores && ulane < slots ? ulane * 2u : kOutOfRange);
+  const uint32_t score32 = buf_load4(sr, !bf16_scores && ulane < slots ? ulane * 4u : kOutOfRange);
+  const uint32_t keep_raw =
+      keeps != nullptr ? buf_load4(make_rsrc(keeps + token, 4u), 0u) : static_cast<uint32_t>(slots);
   float shared_in = 0.0f, gate_in = 0.0f;
   if (shared_mode == kSharedY || shared_mode == kSharedParts)
     shared_in = TT::load(shared_vec[static_cast<uint64_t>(token) * hidden + min(row, hidden - 1u)]);
   if (shared_mode == kSharedParts || with_shared_expert) gate_in = bf16_to_f32(shared_gate[token]);
 
-  for (uint32_t base = wave; base < n_act; base += kWaves * SPW) {
+  uint32_t keep = slots, n_act = n_src;
+  for (uint32_t base = wave; base < n_src; base += kWaves * SPW) {
     XLane<TT> xl[SPW][CPL];
     RowLoad<CPL> rw[SPW];
-    uint32_t word[SPW];
 #pragma unroll
-    for (int i = 0; i < SPW; ++i) {  // route words and activations first
+    for (int i = 0; i < SPW; ++i) {  // activations first (independent of the route words)
       const uint32_t a = base + kWaves * i;
-      word[i] = routes[pair0 + min(a, slots - 1u)];
-      const uint64_t pair = a < keep ? pair0 + a : static_cast<uint64_t>(routed_pairs) + token;
-      issue_x<TT, SW, CPL>(xl[i], x_rsrc<TT>(act + pair * inter, inter), inter, li, a < n_act);
+      const uint64_t pair = a < first_routed ? static_cast<uint64_t>(routed_pairs) + token : pair0 + (a - first_routed);
+      issue_x<TT, SW, CPL>(xl[i], x_rsrc<TT>(act + pair * inter, inter), inter, li, a < n_src);
     }
+    keep = min(uniform(keep_raw), slots);
+    n_act = keep + first_routed;
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {  // then the weight rows
       const uint32_t a = base + kWaves * i;
       ExpertPtrs e{nullptr, nullptr, nullptr, false};
-      if (a < keep) e = expert_ptrs(down, word[i], hidden, inter, group, dense_count);
-      else if (a < n_act) e = expert_ptrs(shared.p[2], 0u, hidden, inter, group, 1u);
+      if (a < first_routed) {
+        e = expert_ptrs(shared.p[2], 0u, hidden, inter, group, 1u);
+      } else if (a < n_act) {
+        const uint32_t word = readlane_u(lane_word, static_cast<int>(a - first_routed));
+        e = expert_ptrs(down, word, hidden, inter, group, dense_count);
+      }
       if (a < n_act && !e.ok && lane == 0) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
       load_row<SW, CPL>(rw[i], expert_rsrc(e, hidden, inter, group), row, inter, group, li, row_ok);
     }
@@ -534,12 +556,18 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(
     }
   }
   __syncthreads();
-  if (wave != 0 || li != 0 || !row_ok) return;
+  if (wave != 0) return;
+  // Scores as wave-uniform values (slot s from lane s), read before the lane mask.
+  const float score_lane = bf16_scores ? bf16_to_f32(score16) : __uint_as_float(score32);
+  float score[kMaxSlots];
+#pragma unroll
+  for (uint32_t s = 0; s < kMaxSlots; ++s) score[s] = readlane_f(score_lane, min(s, kMaxSlots - 1u));
+  if (li != 0 || !row_ok) return;
 
   float acc = 0.0f;
 #pragma unroll
   for (uint32_t s = 0; s < kMaxSlots; ++s)
-    if (s < keep) acc = __fadd_rn(acc, __fmul_rn(dsum[s][sub], score[s]));
+    if (s < keep) acc = __fadd_rn(acc, __fmul_rn(dsum[s + first_routed][sub], score[s]));
   const float routed = TT::round(acc);
   float final_value = routed;
   if (shared_mode == kSharedY) {
@@ -547,7 +575,7 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(
   } else if (shared_mode == kSharedParts) {
     final_value = __fadd_rn(routed, TT::round(__fmul_rn(shared_in, gate_in)));
   } else if (with_shared_expert) {
-    final_value = __fadd_rn(routed, TT::round(__fmul_rn(dsum[keep][sub], gate_in)));
+    final_value = __fadd_rn(routed, TT::round(__fmul_rn(dsum[0][sub], gate_in)));
   }
   out[static_cast<uint64_t>(token) * hidden + row] = TT::store(final_value);
 }

@@ -83,18 +83,35 @@ struct SelectLane {
   uint32_t keep;
 };
 
-// Top-k over unique keys: k rounds of "wave max of the lanes' best key".
-// Lane j keeps the j-th selected key (descending); other lanes get 0.
-__device__ __forceinline__ uint32_t select_keys(uint32_t *key, uint32_t k, int lane) {
+// Sorts a lane's eight keys in descending order (19 compare-exchanges,
+// depth 6).
+__device__ __forceinline__ void sort8_desc(uint32_t (&key)[kSelMaxPerLane]) {
+  constexpr int kNet[19][2] = {{0, 2}, {1, 3}, {4, 6}, {5, 7}, {0, 4}, {1, 5}, {2, 6}, {3, 7}, {0, 1}, {2, 3},
+                               {4, 5}, {6, 7}, {2, 4}, {3, 5}, {1, 4}, {3, 6}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+  for (int c = 0; c < 19; ++c) {
+    const uint32_t a = key[kNet[c][0]], b = key[kNet[c][1]];
+    key[kNet[c][0]] = max(a, b);
+    key[kNet[c][1]] = min(a, b);
+  }
+}
+
+// Top-k over unique keys.  Each lane sorts its keys; round j takes the wave
+// max of the lanes' heads and the winning lane pops its head.  Lane j keeps
+// the j-th selected key (descending); other lanes get 0.  `key` is consumed.
+__device__ __forceinline__ uint32_t select_keys(uint32_t (&key)[kSelMaxPerLane], uint32_t k, int lane) {
+  sort8_desc(key);
   uint32_t mine = 0u;
-  for (uint32_t j = 0; j < k; ++j) {
-    uint32_t best = 0u;
 #pragma unroll
-    for (int i = 0; i < kSelMaxPerLane; ++i) best = key[i] > best ? key[i] : best;
-    best = wave_max_u32_uniform(best);
-    mine = static_cast<uint32_t>(lane) == j ? best : mine;
+  for (uint32_t j = 0; j < static_cast<uint32_t>(kSelMaxTopK); ++j) {
+    if (j < k) {  // wave-uniform
+      const uint32_t best = wave_max_u32_uniform(key[0]);
+      mine = static_cast<uint32_t>(lane) == j ? best : mine;
+      const bool win = key[0] == best;
 #pragma unroll
-    for (int i = 0; i < kSelMaxPerLane; ++i) key[i] = key[i] == best ? 0u : key[i];
+      for (int i = 0; i < kSelMaxPerLane - 1; ++i) key[i] = win ? key[i + 1] : key[i];
+      key[kSelMaxPerLane - 1] = win ? 0u : key[kSelMaxPerLane - 1];
+    }
   }
   return mine;
 }
@@ -207,24 +224,32 @@ __device__ __forceinline__ SelectLane select_token(const SelectParams &a, uint32
     }
     mine = select_keys(key, k, lane);
   }
-  // Lane j < k: slot j.  Reductions over slots run in slot order (readlane).
+  // Lane j < k: slot j.  Reductions over slots run in slot order (the
+  // readlanes are unrolled and independent; only the adds chain).
   const bool slot_lane = static_cast<uint32_t>(lane) < k;
   uint32_t ind = 0xffffu - (mine & 0xffffu);
   const float raw = slot_lane ? bf16_to_f32(static_cast<uint16_t>(mine >> 16)) : 0.0f;
+  float raws[kSelMaxTopK];
+#pragma unroll
+  for (int j = 0; j < kSelMaxTopK; ++j) raws[j] = readlane_f(raw, static_cast<uint32_t>(j));
   float mass32 = 0.0f;
-  for (uint32_t j = 0; j < k; ++j) mass32 = __fadd_rn(mass32, readlane_f(raw, j));
+#pragma unroll
+  for (uint32_t j = 0; j < static_cast<uint32_t>(kSelMaxTopK); ++j)
+    if (j < k) mass32 = __fadd_rn(mass32, raws[j]);
   const float mass = round_bf16(mass32);
   uint32_t keep = k;
   if (a.threshold < 1.0f) {
     double total = 0.0;
-    for (uint32_t j = 0; j < k; ++j) total += static_cast<double>(readlane_f(raw, j));
+#pragma unroll
+    for (uint32_t j = 0; j < static_cast<uint32_t>(kSelMaxTopK); ++j)
+      if (j < k) total += static_cast<double>(raws[j]);
     double accumulated = 0.0;
     uint32_t found = k;
-    for (uint32_t j = 0; j < k; ++j) {
-      accumulated += static_cast<double>(readlane_f(raw, j)) / total;
-      if (accumulated >= static_cast<double>(a.threshold)) {
-        found = j + 1;
-        break;
+#pragma unroll
+    for (uint32_t j = 0; j < static_cast<uint32_t>(kSelMaxTopK); ++j) {
+      if (j < k && found == k) {
+        accumulated += static_cast<double>(raws[j]) / total;
+        if (accumulated >= static_cast<double>(a.threshold)) found = j + 1;
       }
     }
     const uint32_t minimum = a.min_keep < 1u ? 1u : (a.min_keep > k ? k : a.min_keep);
@@ -235,8 +260,13 @@ __device__ __forceinline__ SelectLane select_token(const SelectParams &a, uint32
   const bool kept = static_cast<uint32_t>(lane) < keep;
   ind = kept ? ind : ind0;
   const float padded = kept ? raw : 0.0f;
-  float sel32 = 0.0f;
-  for (uint32_t j = 0; j < k; ++j) sel32 = __fadd_rn(sel32, readlane_f(padded, j));
+  float sel32 = mass32;  // every slot kept: the same sum in the same order
+  if (keep < k) {
+    sel32 = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < static_cast<uint32_t>(kSelMaxTopK); ++j)
+      if (j < k) sel32 = __fadd_rn(sel32, j < keep ? raws[j] : 0.0f);
+  }
   const float selected = round_bf16(sel32);
   const float blend = round_bf16(a.blend);
   const float norm = badd(mass, bmul(blend, bsub(selected, mass)));

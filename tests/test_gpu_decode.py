@@ -344,10 +344,15 @@ def test_fused_routed_layer_matches_unfused_and_oracle(torch_mod, records, share
     layer.launch(None)
     torch.cuda.synchronize()
     fused = layer.out.clone()
-    fused_routes = layer.routes.clone()
+    published = [t.clone() for t in (layer.routes, layer.inds, layer.scores, layer.shared_gate)]
+    if threshold < 1:
+        published.append(layer.keeps.clone())
     layer.launch_unfused(None)
     torch.cuda.synchronize()
-    assert torch.equal(fused_routes, layer.routes)
+    again = [layer.routes, layer.inds, layer.scores, layer.shared_gate] + ([layer.keeps] if threshold < 1 else [])
+    for a, b in zip(published, again):
+        assert torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                           b.view(torch.int16) if b.dtype == torch.bfloat16 else b)
     assert torch.equal(fused.view(torch.int16), layer.out.view(torch.int16))
     from flashnext_hip import _lib
 
@@ -360,6 +365,75 @@ def test_fused_routed_layer_matches_unfused_and_oracle(torch_mod, records, share
     want = moe.decode_layer(x, ref["inds"], ref["scores"], recs, score_dtype="bf16", shared_gate_weight=wsg,
                             keeps=ref["keeps"] if threshold < 1 else None)
     assert_close(bf16.bf16_to_f32(from_dev_bf16(fused)), bf16.bf16_to_f32(want), "fused routed layer")
+
+
+def _routed_layer(torch, records, shared_records, tokens, top_k, threshold, seed):
+    from flashnext_hip.layout import make_layout
+    from flashnext_hip.moe_block import DecodeLayer, LayerWeights
+
+    slots = 24
+    perm = np.random.default_rng(seed).permutation(slots)[:E].astype(np.int32)
+    img, _ = pool_from_banks(records, perm, slots, H, I)
+    sh = tuple(tuple(t[:1] for t in to_dev_bank(b)) for b in (shared_records.gate, shared_records.up,
+                                                               shared_records.down))
+    weights = LayerWeights(make_layout(H, I), torch.from_numpy(img).cuda(), torch.from_numpy(perm).cuda(),
+                           to_dev_bf16(bf16_normal((E, H), seed=seed + 1, std=0.02)),
+                           to_dev_bf16(bf16_normal((1, H), seed=seed + 2, std=0.02)).reshape(-1), sh)
+    return DecodeLayer(weights, tokens, top_k, threshold=threshold, min_keep=2)
+
+
+def test_routed_layer_repeated_launches_graph_replays_and_mixed_shapes(torch_mod, records, shared_records):
+    """The routed layer entry point (router + selection folded into gate/up +
+    down) must match the separate router and expert calls bit for bit across
+    back-to-back eager launches, graph replays with fresh tokens between
+    replays, and layers of different slot counts and keep thresholds run in
+    turn, with no device error flag raised."""
+    torch = torch_mod
+    from flashnext_hip import _lib
+
+    layers = [_routed_layer(torch, records, shared_records, 1, 10, 1.0, 170),
+              _routed_layer(torch, records, shared_records, 1, 8, 1.0, 180),
+              _routed_layer(torch, records, shared_records, 1, 10, 0.85, 190)]
+    rng = np.random.default_rng(175)
+
+    def check(layer, tag):
+        fused = layer.out.clone()
+        routes = layer.routes.clone()
+        layer.launch_unfused(None)
+        torch.cuda.synchronize()
+        assert torch.equal(routes, layer.routes), tag
+        assert torch.equal(fused.view(torch.int16), layer.out.view(torch.int16)), tag
+
+    for it in range(4):
+        for n, layer in enumerate(layers):
+            say(f"case: eager fused launch iteration {it} layer {n}")
+            layer.x.copy_(to_dev_bf16(bf16.f32_to_bf16(rng.normal(0, 1, (1, H)).astype(np.float32))))
+            layer.launch(None)
+            torch.cuda.synchronize()
+            check(layer, f"eager it={it} layer={n}")
+    assert _lib.check_device_errors() == 0
+    stream = torch.cuda.Stream()
+    handle = stream.cuda_stream
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        for layer in layers:
+            layer.launch(handle)
+    for rep in range(4):
+        say(f"case: graph replay {rep} of three fused layers")
+        xs = [to_dev_bf16(bf16.f32_to_bf16(rng.normal(0, 1, (1, H)).astype(np.float32))) for _ in layers]
+        for layer, xv in zip(layers, xs):
+            layer.x.copy_(xv)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        outs = [layer.out.clone() for layer in layers]
+        for n, (layer, o) in enumerate(zip(layers, outs)):
+            layer.launch_unfused(None)
+            torch.cuda.synchronize()
+            assert torch.equal(o.view(torch.int16), layer.out.view(torch.int16)), f"replay {rep} layer {n}"
+    assert _lib.check_device_errors() == 0
 
 
 def test_out_of_range_route_word_is_skipped_and_flagged(torch_mod, records, dev_records):
