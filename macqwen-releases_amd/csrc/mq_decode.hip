@@ -665,21 +665,67 @@ int launch_gather_qmv(const void *x, int slot_input, const MqProjection &proj, c
   return check_launch("gather_qmv_kernel");
 }
 
+// Blocks of `kernel` that can be resident at once on the current device
+// (cached per kernel and device).
+template <const void *(*KERNEL)()>
+int64_t resident_blocks() {
+  static int64_t cached[64];
+  static bool known[64];
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return 0;
+  if (!known[device]) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, KERNEL(), kThreads, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+      return 0;
+    cached[device] = static_cast<int64_t>(per_cu) * cus;
+    known[device] = true;
+  }
+  return cached[device];
+}
+
+template <class TT, int SW, int CPL, int R, bool SELECT>
+const void *gateup_ptr() {
+  return reinterpret_cast<const void *>(gateup_kernel<TT, SW, CPL, R, SELECT>);
+}
+
+template <class TT, int SW, int CPL, int R, bool SELECT>
+void launch_gateup_r(const MqMoeArgs &a, const SharedExpert &shared, bool has_shared, const int32_t *keeps,
+                     const SelectParams &sel, const SelectOutputs &sel_out, typename TT::storage *act,
+                     unsigned int *err, uint32_t pairs, hipStream_t stream) {
+  using S = typename TT::storage;
+  constexpr int kTileRows = R * Slice<SW>::kRows;
+  const uint32_t tiles = pairs * ceil_div(a.inter, kTileRows);
+  hipLaunchKernelGGL((gateup_kernel<TT, SW, CPL, R, SELECT>), dim3(ceil_div(tiles, kWaves)), dim3(kThreads), 0,
+                     stream, static_cast<const S *>(a.x), a.gate, a.up, shared, has_shared, a.routes, keeps, sel,
+                     sel_out, act, static_cast<S *>(a.gate_out), static_cast<S *>(a.up_out), a.tokens, a.slots,
+                     a.hidden, a.inter, a.group_size, a.expert_count, tiles, err);
+}
+
+// Gate/up launch.  With routes given and 64-lane slices, a wave takes 2, 4 or
+// 8 rows per tile: the smallest count whose grid is resident at once, so that
+// many-token calls (speculative verify) stream in one round of blocks rather
+// than in successive rounds that each pay the full memory latency.
 template <class TT, bool SELECT>
 int launch_gateup(const MqMoeArgs &a, const SharedExpert &shared, bool has_shared, const int32_t *keeps,
                   const SelectParams &sel, const SelectOutputs &sel_out, typename TT::storage *act,
                   unsigned int *err, hipStream_t stream) {
-  using S = typename TT::storage;
   const Geometry g = geometry(a.hidden);
   const uint32_t pairs = a.tokens * a.slots + (has_shared ? a.tokens : 0u);
   MQ_GEOM_SWITCH(g, {
-    constexpr int R = steps_for<SW>();
-    constexpr int kTileRows = R * Slice<SW>::kRows;
-    const uint32_t tiles = pairs * ceil_div(a.inter, kTileRows);
-    hipLaunchKernelGGL((gateup_kernel<TT, SW, CPL, R, SELECT>), dim3(ceil_div(tiles, kWaves)), dim3(kThreads), 0,
-                       stream, static_cast<const S *>(a.x), a.gate, a.up, shared, has_shared, a.routes, keeps, sel,
-                       sel_out, act, static_cast<S *>(a.gate_out), static_cast<S *>(a.up_out), a.tokens, a.slots,
-                       a.hidden, a.inter, a.group_size, a.expert_count, tiles, err);
+    if constexpr (SW == 64 && !SELECT) {
+      const auto blocks = [&](uint32_t r) { return static_cast<int64_t>(ceil_div(pairs * ceil_div(a.inter, r), kWaves)); };
+      if (blocks(2) <= resident_blocks<gateup_ptr<TT, SW, CPL, 2, false>>()) {
+        launch_gateup_r<TT, SW, CPL, 2, false>(a, shared, has_shared, keeps, sel, sel_out, act, err, pairs, stream);
+      } else if (blocks(4) <= resident_blocks<gateup_ptr<TT, SW, CPL, 4, false>>()) {
+        launch_gateup_r<TT, SW, CPL, 4, false>(a, shared, has_shared, keeps, sel, sel_out, act, err, pairs, stream);
+      } else {
+        launch_gateup_r<TT, SW, CPL, 8, false>(a, shared, has_shared, keeps, sel, sel_out, act, err, pairs, stream);
+      }
+    } else {
+      constexpr int R = steps_for<SW>();
+      launch_gateup_r<TT, SW, CPL, R, SELECT>(a, shared, has_shared, keeps, sel, sel_out, act, err, pairs, stream);
+    }
   });
   return check_launch("gateup_kernel");
 }
@@ -944,6 +990,15 @@ extern "C" int mq_moe_layer(const MqRouteArgs *route, const MqMoeArgs *moe, void
   a.keeps = r.keeps;
   if ((rc = validate_moe_args(a, true))) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (r.tokens >= 2) {
+    // Several tokens: one selection pass, then the expert kernels with routes
+    // given.  Folding the selection into every gate/up block (as for one
+    // token) would make the larger grid run in several rounds of blocks,
+    // each repeating the selection's latency.
+    if ((rc = mq_route_topk(&r, stream))) return rc;
+    if (r.threshold >= 1.0f) a.keeps = nullptr;
+    return moe_decode_t<BF16T>(a, s, nullptr, nullptr);
+  }
   rc = launch_router_logits(r.x, r.gate_w, r.shared_gate != nullptr ? r.shared_gate_w : nullptr, r.logits_out,
                             r.shared_gate, r.tokens, r.hidden, r.experts, s);
   if (rc) return rc;
