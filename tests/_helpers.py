@@ -102,3 +102,61 @@ def pool_from_banks(records, slot_of_expert, slots: int, hidden: int, inter: int
                 start = base + offs[f"{proj}.{part}"]
                 img[start:start + payload.size] = payload
     return img, stride
+
+
+def write_safetensors(path, tensors) -> None:
+    """Write a safetensors file: ``tensors`` maps name -> (dtype tag, array)
+    (an 8-byte little-endian header length, the JSON header, then the data)."""
+    import json
+    import struct
+
+    header, blobs, offset = {}, [], 0
+    for name, (dtype, arr) in tensors.items():
+        data = np.ascontiguousarray(arr).tobytes()
+        header[name] = {"dtype": dtype, "shape": list(arr.shape), "data_offsets": [offset, offset + len(data)]}
+        blobs.append(data)
+        offset += len(data)
+    head = json.dumps(header).encode()
+    head += b" " * (-len(head) % 8)
+    with open(path, "wb") as handle:
+        handle.write(struct.pack("<Q", len(head)))
+        handle.write(head)
+        for data in blobs:
+            handle.write(data)
+
+
+def write_moe_checkpoint(directory, layers, *, experts: int, hidden: int, inter: int, groups, seed: int,
+                         shared: bool = True):
+    """A sharded checkpoint with the model's MoE tensor names: one shard per
+    layer plus ``model.safetensors.index.json``.  ``groups[l]`` is layer l's
+    quantisation group.  Returns {layer: dict of the arrays written}."""
+    import json
+    import os
+
+    weight_map, written = {}, {}
+    for layer in range(layers):
+        group = groups[layer]
+        base = f"language_model.model.layers.{layer}.mlp"
+        recs = make_records(experts, hidden, inter, seed + 10 * layer, group)
+        tensors = {}
+        for proj, bank in (("gate_proj", recs.gate), ("up_proj", recs.up), ("down_proj", recs.down)):
+            tensors[f"{base}.switch_mlp.{proj}.weight"] = ("U32", bank.packed.view(np.uint32))
+            tensors[f"{base}.switch_mlp.{proj}.scales"] = ("BF16", bank.scales)
+            tensors[f"{base}.switch_mlp.{proj}.biases"] = ("BF16", bank.biases)
+        tensors[f"{base}.gate.weight"] = ("BF16", bf16_normal((experts, hidden), seed + 10 * layer + 5, 0.02))
+        sh = None
+        if shared:
+            sh = make_records(1, hidden, inter, seed + 10 * layer + 6, group)
+            for proj, bank in (("gate_proj", sh.gate), ("up_proj", sh.up), ("down_proj", sh.down)):
+                tensors[f"{base}.shared_expert.{proj}.weight"] = ("U32", bank.packed[0].view(np.uint32))
+                tensors[f"{base}.shared_expert.{proj}.scales"] = ("BF16", bank.scales[0])
+                tensors[f"{base}.shared_expert.{proj}.biases"] = ("BF16", bank.biases[0])
+            tensors[f"{base}.shared_expert_gate.weight"] = ("BF16", bf16_normal((1, hidden), seed + 10 * layer + 7,
+                                                                                0.02))
+        shard = f"model-{layer + 1:05d}-of-{layers:05d}.safetensors"
+        write_safetensors(os.path.join(directory, shard), tensors)
+        weight_map.update({name: shard for name in tensors})
+        written[layer] = {"records": recs, "shared": sh, "tensors": tensors}
+    with open(os.path.join(directory, "model.safetensors.index.json"), "w") as handle:
+        json.dump({"metadata": {}, "weight_map": weight_map}, handle)
+    return written
