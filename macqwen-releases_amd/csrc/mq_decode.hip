@@ -979,7 +979,6 @@ extern "C" int mq_moe_layer(const MqRouteArgs *route, const MqMoeArgs *moe, void
   if (moe->x_dtype != MQ_BF16 || moe->x != r.x) return fail(MQ_ERR_INVALID, "the routed layer needs the same bf16 x");
   if (r.tokens != moe->tokens || r.top_k != moe->slots || r.hidden != moe->hidden)
     return fail(MQ_ERR_INVALID, "route and moe shapes disagree");
-  if (r.tokens > kMaxLayerTokens) return fail(MQ_ERR_INVALID, "the routed layer handles at most %u tokens", kMaxLayerTokens);
   if (moe->flags != 0) return fail(MQ_ERR_INVALID, "the routed layer supports no MQ_DECODE flags");
   if ((moe->shared_expert != nullptr) != (r.shared_gate != nullptr))
     return fail(MQ_ERR_INVALID, "a shared expert needs the router's shared_gate output and vice versa");

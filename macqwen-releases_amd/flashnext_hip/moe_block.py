@@ -122,3 +122,73 @@ class DecodeLayer:
 
     def launch_experts(self, stream):
         _lib.check(self._lib.mq_moe_decode(self.moe_args, stream), self._lib)
+
+
+class MoEBlock:
+    """``_moe_call`` for any token count (``adaptive_topk.py:53-292``).
+
+    Up to ``fused_max_tokens`` tokens (8, the bound under which the reference
+    hands the scores to the fused executor, ``adaptive_topk.py:266-269``) the
+    block runs a :class:`DecodeLayer` per token count: router, experts and the
+    ordered float32 combine with ``shared_y`` in the down kernel.  Beyond it
+    the router runs on its own and the (token, slot) rows go through the
+    grouped path (``switch_mlp(x, inds)``), combined in bf16 as
+    ``(y * scores).sum(-2) + shared_gate * shared`` (``adaptive_topk.py:274-277``).
+    At a keep threshold below 1 the dropped slots carry the row's first expert
+    and score 0 on both paths (``adaptive_topk.py:213-227``).
+
+    ``last_path`` is ``"fused"`` or ``"grouped"`` after each call.
+    """
+
+    def __init__(self, weights: LayerWeights, top_k: int, *, threshold: float = 1.0, min_keep: int = 1,
+                 blend: float = 1.0, fused_max_tokens: int = 8):
+        from .grouped import GroupedMoE
+
+        if not 0 <= fused_max_tokens <= 8:
+            raise ValueError("fused_max_tokens must be in 0..8")
+        self.w = weights
+        self.top_k, self.threshold, self.min_keep, self.blend = int(top_k), float(threshold), int(min_keep), float(blend)
+        self.fused_max_tokens = int(fused_max_tokens)
+        self.device = weights.pool.device
+        self.hidden, self.inter = weights.layout.hidden, weights.layout.inter
+        self._layers: dict[int, DecodeLayer] = {}
+        lay = weights.layout
+        self._grouped = GroupedMoE(pool_projection(weights.pool, lay, "gate_proj"),
+                                   pool_projection(weights.pool, lay, "up_proj"),
+                                   pool_projection(weights.pool, lay, "down_proj"),
+                                   hidden=lay.hidden, inter=lay.inter, group_size=lay.group_size,
+                                   shared_expert=weights.shared)
+        self._pool = weights.pool  # the projection structs hold its address
+        self.last_path = None
+        self.last_route = None
+
+    def __call__(self, x: torch.Tensor) -> torch.Tensor:
+        """``x``: bf16 ``[T, hidden]`` on the block's device -> bf16 ``[T, hidden]``."""
+        from .router import route
+
+        if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[1] != self.hidden:
+            raise ValueError(f"x must be bf16 [tokens, {self.hidden}]")
+        if x.device != self.device:
+            raise ValueError(f"x is on {x.device}, the block on {self.device}")
+        tokens = int(x.shape[0])
+        if tokens == 0:
+            raise ValueError("x has no tokens")
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        if tokens <= self.fused_max_tokens:
+            layer = self._layers.get(tokens)
+            if layer is None:
+                layer = DecodeLayer(self.w, tokens, self.top_k, threshold=self.threshold, min_keep=self.min_keep,
+                                    blend=self.blend, device=self.device)
+                self._layers[tokens] = layer
+            layer.x.copy_(x)
+            layer.launch(stream)
+            self.last_path = "fused"
+            self.last_route = layer
+            return layer.out.clone()
+        r = route(x, self.w.router_w, self.top_k, threshold=self.threshold, min_keep=self.min_keep,
+                  blend=self.blend, slot_table=self.w.slot_table, shared_gate_w=self.w.shared_gate_w,
+                  keep_logits=False)
+        out, _y = self._grouped(x, r.routes, r.scores, shared_gate=r.shared_gate)
+        self.last_path = "grouped"
+        self.last_route = r
+        return out

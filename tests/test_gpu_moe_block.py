@@ -1,0 +1,153 @@
+"""GPU parity of the ``_moe_call`` composition at every token count, and the
+segmented-equals-single premise of the sorted prefill path.
+
+``MoEBlock`` runs up to 8 tokens through the routed decode layer (ordered
+float32 combine, ``adaptive_topk.py:266-292``) and more through the router +
+grouped path with the bf16 generic combine (``adaptive_topk.py:274-277``).
+Routes are compared bit for bit with ``oracle.router.route``; outputs with
+``oracle.moe.decode_layer`` or ``oracle.moe.prefill_layer`` at the layer
+tolerance (rtol 1e-2, atol 3e-3, max rel 1e-2, cosine 0.9999).
+
+The segmented test restates ``models/flashnext/tests/unit/test_prefill_pipeline_math.py:21-54``:
+the (token, slot) rows sorted by expert and computed in contiguous expert
+chunks must give the bits of one call over all rows.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import bf16, moe, router as orouter
+
+from ._helpers import (MAX_REL, MIN_COSINE, assert_close, bf16_normal, from_dev_bf16, make_records,
+                       pool_from_banks, say, to_dev_bank, to_dev_bf16, value_report)
+
+pytestmark = pytest.mark.gpu
+
+H, I, E, K = 2048, 512, 16, 10
+
+
+@pytest.fixture(scope="module")
+def torch_mod():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    from flashnext_hip import _lib
+
+    lib = _lib.load()
+    assert lib.mq_available() == 1, _lib.last_error(lib)
+    return torch
+
+
+@pytest.fixture(scope="module")
+def layer(torch_mod):
+    torch = torch_mod
+    from flashnext_hip.layout import make_layout
+    from flashnext_hip.moe_block import LayerWeights
+
+    records = make_records(E, H, I, seed=500)
+    shared = make_records(1, H, I, seed=501)
+    slots = 24
+    perm = np.random.default_rng(502).permutation(slots)[:E].astype(np.int32)
+    img, _ = pool_from_banks(records, perm, slots, H, I)
+    wg = bf16_normal((E, H), seed=503, std=0.02)
+    wsg = bf16_normal((1, H), seed=504, std=0.02)
+    sh = tuple(tuple(t[:1] for t in to_dev_bank(b)) for b in (shared.gate, shared.up, shared.down))
+    weights = LayerWeights(make_layout(H, I), torch.from_numpy(img).cuda(), torch.from_numpy(perm).cuda(),
+                           to_dev_bf16(wg), to_dev_bf16(wsg).reshape(-1), sh)
+    recs = moe.ExpertRecordSet(records.gate, records.up, records.down, shared=(shared.gate, shared.up, shared.down))
+    return weights, recs, perm, wg, wsg
+
+
+@pytest.mark.parametrize("tokens,threshold", [(1, 1.0), (5, 0.85), (8, 1.0), (9, 1.0), (40, 0.85), (130, 1.0)])
+def test_moe_block_matches_oracle_on_both_paths(torch_mod, layer, tokens, threshold):
+    torch = torch_mod
+    say(f"case: moe block tokens={tokens} threshold={threshold}")
+    from flashnext_hip import _lib
+    from flashnext_hip.moe_block import MoEBlock
+
+    weights, recs, perm, wg, wsg = layer
+    block = MoEBlock(weights, K, threshold=threshold, min_keep=2)
+    x = bf16_normal((tokens, H), seed=510 + tokens)
+    out = block(to_dev_bf16(x))
+    torch.cuda.synchronize()
+    assert _lib.check_device_errors() == 0
+    assert block.last_path == ("fused" if tokens <= 8 else "grouped")
+    ref = orouter.route(x, wg, K, threshold=threshold, min_keep=2, slot_table=perm.astype(np.uint32))
+    r = block.last_route
+    assert np.array_equal(r.routes.cpu().numpy().view(np.uint32), ref["routes"])
+    assert np.array_equal(from_dev_bf16(r.scores), ref["scores"])
+    got = bf16.bf16_to_f32(from_dev_bf16(out))
+    if tokens <= 8:
+        want = moe.decode_layer(x, ref["inds"], ref["scores"], recs, score_dtype="bf16", shared_gate_weight=wsg,
+                                keeps=ref["keeps"] if threshold < 1 else None)
+        assert_close(got, bf16.bf16_to_f32(want), f"fused block T={tokens}")
+        return
+    width = ref["width"]
+    tiles, _ = moe.prefill_layer(x, ref["inds"][:, :width], ref["scores"][:, :width], recs,
+                                 shared_gate_weight=wsg, weights="bf16")
+    exact, _ = moe.prefill_layer(x, ref["inds"][:, :width], ref["scores"][:, :width], recs,
+                                 shared_gate_weight=wsg)
+    assert_close(got, bf16.bf16_to_f32(tiles), f"grouped block T={tokens} (bf16 tiles)")
+    rep = value_report(got, bf16.bf16_to_f32(exact))
+    assert rep["cosine"] >= MIN_COSINE and rep["max_rel"] <= MAX_REL, rep
+    # a second call at the same size reuses the grouped workspace and gives the same bits
+    again = block(to_dev_bf16(x))
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+
+
+def test_routed_layer_sixteen_tokens_matches_separate_calls(torch_mod, layer):
+    torch = torch_mod
+    say("case: routed layer entry point at 16 tokens")
+    from flashnext_hip.moe_block import DecodeLayer
+
+    weights, recs, perm, wg, wsg = layer
+    dl = DecodeLayer(weights, 16, K)
+    x = bf16_normal((16, H), seed=520)
+    dl.x.copy_(to_dev_bf16(x))
+    dl.launch(None)
+    torch.cuda.synchronize()
+    out, routes = dl.out.clone(), dl.routes.clone()
+    dl.launch_unfused(None)
+    torch.cuda.synchronize()
+    assert torch.equal(routes, dl.routes)
+    assert torch.equal(out.view(torch.int16), dl.out.view(torch.int16))
+    ref = orouter.route(x, wg, K, slot_table=perm.astype(np.uint32))
+    want = moe.decode_layer(x, ref["inds"], ref["scores"], recs, score_dtype="bf16", shared_gate_weight=wsg)
+    assert_close(bf16.bf16_to_f32(from_dev_bf16(out)), bf16.bf16_to_f32(want), "routed layer T=16")
+
+
+def test_segmented_sorted_rows_equal_one_call(torch_mod):
+    torch = torch_mod
+    say("case: segmented grouped rows T=96 K=8 E=40 H=2560 I=640")
+    from flashnext_hip.grouped import GroupedMoE
+
+    tokens, slots, hidden, inter, experts, chunk = 96, 8, 2560, 640, 40, 11
+    records = make_records(experts, hidden, inter, seed=530)
+    x = bf16.f32_to_bf16((np.random.default_rng(531).normal(0, 0.5, (tokens, hidden))).astype(np.float32))
+    inds = np.random.default_rng(532).integers(0, experts, (tokens, slots))
+    banks = tuple(to_dev_bank(b) for b in (records.gate, records.up, records.down))
+    xd = to_dev_bf16(x)
+    _, y_all = GroupedMoE(*banks, hidden=hidden, inter=inter)(xd, torch.from_numpy(inds.astype(np.int32)).cuda(),
+                                                              combine=False)
+    flat = inds.reshape(-1)
+    order = np.argsort(flat, kind="stable")  # the sorted (token, slot) rows
+    y_seg = torch.zeros_like(y_all)
+    done = 0
+    for start in range(0, experts, chunk):
+        end = min(experts, start + chunk)
+        rows = order[(flat[order] >= start) & (flat[order] < end)]
+        if rows.size == 0:
+            continue
+        seg_banks = tuple(tuple(t[start:end] for t in bank) for bank in banks)
+        g = GroupedMoE(*seg_banks, hidden=hidden, inter=inter)
+        local = torch.from_numpy((flat[rows] - start).astype(np.int32).reshape(-1, 1)).cuda()
+        t_idx = torch.from_numpy(rows // slots).cuda()
+        s_idx = torch.from_numpy(rows % slots).cuda()
+        _, y_c = g(xd[t_idx].contiguous(), local, combine=False)
+        y_seg[t_idx, s_idx] = y_c[:, 0]
+        done += rows.size
+    torch.cuda.synchronize()
+    assert done == tokens * slots
+    assert torch.equal(y_all.view(torch.int16), y_seg.view(torch.int16))
