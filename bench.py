@@ -258,11 +258,9 @@ def verify_bench(torch, dev, runners, stream, tokens: int, reps: int = 10) -> di
         v = DecodeLayer(r.w, tokens, TOP_K, device=dev)
         v.x.copy_(torch.randn(v.x.shape, generator=gen, device=dev).to(torch.bfloat16))
         rs.append(v)
-    fused = tokens <= 8  # the routed-layer entry point takes up to 8 tokens
-
     def run():
         for v in rs:
-            (v.launch if fused else v.launch_unfused)(handle)
+            v.launch(handle)
 
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
@@ -274,7 +272,7 @@ def verify_bench(torch, dev, runners, stream, tokens: int, reps: int = 10) -> di
     ms = time_graph(torch, g, reps, stream) / (reps * len(rs))
     nbytes = (sum(unique) / len(unique) + 1) * expert_bytes_per_record()
     del g, rs
-    return {"tokens": tokens, "path": "mq_moe_layer" if fused else "mq_route_topk + mq_moe_decode",
+    return {"tokens": tokens, "path": "mq_moe_layer",
             "us_per_layer": round(ms * 1000, 3), "us_per_token": round(ms * 1000 / tokens, 3),
             "unique_experts_mean": round(sum(unique) / len(unique), 2), "expert_bytes_per_layer": int(nbytes),
             "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
@@ -391,6 +389,7 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true", help="skip the QMV / verify / stack / peak rows")
     ap.add_argument("--pmc-pass", action="store_true", help="eager launches for rocprofv3 --pmc, no timing")
     ap.add_argument("--prefill-only", action="store_true", help="time only the 4096-token prefill grouped path")
+    ap.add_argument("--verify-only", action="store_true", help="time only the 4- and 16-token verify layers")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the expert-parallel "
@@ -430,6 +429,9 @@ def main() -> int:
     torch.cuda.synchronize()
     if args.pmc_pass:
         pmc_pass(torch, runners, stream, handle)
+        return 0
+    if args.verify_only:
+        print(json.dumps({"verify": [verify_bench(torch, dev, runners, stream, t) for t in (4, 16)]}), flush=True)
         return 0
     log("capturing graphs")
     g_all = capture(torch, lambda: [r.launch(handle) for r in runners], stream)

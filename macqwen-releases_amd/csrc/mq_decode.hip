@@ -472,7 +472,7 @@ enum SharedMode : int { kSharedNone = 0, kSharedY = 1, kSharedParts = 2, kShared
 // order: acc += float(d) * float(score[t,s]) in float32 with no contraction
 // (models/flashnext/metal_runtime.py:291-336), then T(acc) and the shared
 // epilogue.  Padded slots (s >= keep) carry score 0 and are skipped.
-template <class TT, int SW, int CPL, int SPW>
+template <class TT, int SW, int CPL, int SPW, int R>
 __global__ __launch_bounds__(kThreads) void down_combine_kernel(
     const typename TT::storage *__restrict__ act, MqProjection down, SharedExpert shared,
     const uint32_t *__restrict__ routes, const void *__restrict__ scores, int score_dtype,
@@ -482,15 +482,19 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(
     unsigned int *__restrict__ err) {
   using Sl = Slice<SW>;
   constexpr uint32_t kMaxSources = kMaxSlots + 1;
-  __shared__ float dsum[kMaxSources][Sl::kRows];
+  constexpr uint32_t kBlockRows = Sl::kRows * R;  // R row groups of kRows rows
+  static_assert(kBlockRows <= 64, "the combine takes one lane per block row");
+  __shared__ float dsum[kMaxSources][kBlockRows];
 
   const int lane = threadIdx.x & 63;
   const uint32_t wave = wave_id();
   const int li = Sl::li(lane);
   const int sub = Sl::sub(lane);
   const uint32_t token = blockIdx.y;
-  const uint32_t row = blockIdx.x * Sl::kRows + sub;
-  const bool row_ok = row < hidden;
+  const uint32_t row0 = blockIdx.x * kBlockRows;  // rows row0 + r * kRows + sub, r < R
+  const uint32_t ulane0 = static_cast<uint32_t>(lane);
+  const uint32_t fin_row = row0 + ulane0;  // the row this lane combines (lanes < kBlockRows)
+  const bool fin_ok = ulane0 < kBlockRows && fin_row < hidden;
   const bool with_shared_expert = shared_mode == kSharedExpert;
   const uint32_t first_routed = with_shared_expert ? 1u : 0u;  // source index of routed slot 0
   const uint32_t n_src = slots + first_routed;                // sources before the keep count is known
@@ -513,13 +517,13 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(
       keeps != nullptr ? buf_load4(make_rsrc(keeps + token, 4u), 0u) : static_cast<uint32_t>(slots);
   float shared_in = 0.0f, gate_in = 0.0f;
   if (shared_mode == kSharedY || shared_mode == kSharedParts)
-    shared_in = TT::load(shared_vec[static_cast<uint64_t>(token) * hidden + min(row, hidden - 1u)]);
+    shared_in = TT::load(shared_vec[static_cast<uint64_t>(token) * hidden + min(fin_row, hidden - 1u)]);
   if (shared_mode == kSharedParts || with_shared_expert) gate_in = bf16_to_f32(shared_gate[token]);
 
   uint32_t keep = slots, n_act = n_src;
   for (uint32_t base = wave; base < n_src; base += kWaves * SPW) {
     XLane<TT> xl[SPW][CPL];
-    RowLoad<CPL> rw[SPW];
+    RowLoad<CPL> rw[SPW][R];
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {  // activations first (independent of the route words)
       const uint32_t a = base + kWaves * i;
@@ -539,19 +543,27 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(
         e = expert_ptrs(down, word, hidden, inter, group, dense_count);
       }
       if (a < n_act && !e.ok && lane == 0) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
-      load_row<SW, CPL>(rw[i], expert_rsrc(e, hidden, inter, group), row, inter, group, li, row_ok);
+      const ExpertRsrc er = expert_rsrc(e, hidden, inter, group);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t row = row0 + static_cast<uint32_t>(r) * Sl::kRows + static_cast<uint32_t>(sub);
+        load_row<SW, CPL>(rw[i][r], er, row, inter, group, li, row < hidden);
+      }
     }
-    float v[SPW];
+    float v[SPW][R];
 #pragma unroll
     for (int i = 0; i < SPW; ++i) {
       finish_x<TT, CPL>(xl[i]);
-      v[i] = Sl::reduce(row_partial<TT, CPL>(rw[i], xl[i]));
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[i][r] = Sl::reduce(row_partial<TT, CPL>(rw[i][r], xl[i]));
     }
     if (li == 0) {
 #pragma unroll
       for (int i = 0; i < SPW; ++i) {
         const uint32_t a = base + kWaves * i;
-        if (a < n_act) dsum[a][sub] = TT::round(v[i]);  // a bad route reads as zero weights: d = 0
+#pragma unroll
+        for (int r = 0; r < R; ++r)  // a bad route reads as zero weights: d = 0
+          if (a < n_act) dsum[a][static_cast<uint32_t>(r) * Sl::kRows + static_cast<uint32_t>(sub)] = TT::round(v[i][r]);
       }
     }
   }
@@ -562,12 +574,12 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(
   float score[kMaxSlots];
 #pragma unroll
   for (uint32_t s = 0; s < kMaxSlots; ++s) score[s] = readlane_f(score_lane, min(s, kMaxSlots - 1u));
-  if (li != 0 || !row_ok) return;
+  if (!fin_ok) return;
 
   float acc = 0.0f;
 #pragma unroll
   for (uint32_t s = 0; s < kMaxSlots; ++s)
-    if (s < keep) acc = __fadd_rn(acc, __fmul_rn(dsum[s + first_routed][sub], score[s]));
+    if (s < keep) acc = __fadd_rn(acc, __fmul_rn(dsum[s + first_routed][ulane0], score[s]));
   const float routed = TT::round(acc);
   float final_value = routed;
   if (shared_mode == kSharedY) {
@@ -575,9 +587,9 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(
   } else if (shared_mode == kSharedParts) {
     final_value = __fadd_rn(routed, TT::round(__fmul_rn(shared_in, gate_in)));
   } else if (with_shared_expert) {
-    final_value = __fadd_rn(routed, TT::round(__fmul_rn(dsum[0][sub], gate_in)));
+    final_value = __fadd_rn(routed, TT::round(__fmul_rn(dsum[0][ulane0], gate_in)));
   }
-  out[static_cast<uint64_t>(token) * hidden + row] = TT::store(final_value);
+  out[static_cast<uint64_t>(token) * hidden + fin_row] = TT::store(final_value);
 }
 
 // ------------------------------------------------------------------ dispatch
@@ -730,16 +742,50 @@ int launch_gateup(const MqMoeArgs &a, const SharedExpert &shared, bool has_share
   return check_launch("gateup_kernel");
 }
 
+template <class TT, int SW, int CPL, int SPW, int R>
+void launch_down_r(const MqMoeArgs &a, const SharedExpert &shared, int shared_mode,
+                   const typename TT::storage *shared_vec, const int32_t *keeps, const typename TT::storage *act,
+                   unsigned int *err, hipStream_t stream) {
+  using S = typename TT::storage;
+  const dim3 grid(ceil_div(a.hidden, Slice<SW>::kRows * R), a.tokens);
+  hipLaunchKernelGGL((down_combine_kernel<TT, SW, CPL, SPW, R>), grid, dim3(kThreads), 0, stream, act, a.down, shared,
+                     a.routes, a.scores, a.score_dtype, keeps, shared_mode, shared_vec, a.shared_gate,
+                     static_cast<S *>(a.out), a.tokens, a.slots, a.hidden, a.inter, a.group_size, a.expert_count,
+                     err);
+}
+
+template <class TT, int SW, int CPL, int SPW, int R>
+const void *down_ptr() {
+  return reinterpret_cast<const void *>(down_combine_kernel<TT, SW, CPL, SPW, R>);
+}
+
+// Down launch for SPW sources per wave.  One token keeps one row group per
+// wave (the grid of the hidden rows is resident at once).  Several tokens
+// take 2, 4 or 8 row groups per wave (bf16, 16-lane slices of at most two
+// chunks per lane, at most three sources per wave): the smallest count whose grid is resident at once,
+// so that a verify batch streams in one round of blocks instead of rounds that
+// each pay the route-word and weight latencies.
 template <class TT, int SW, int CPL, int SPW>
 void launch_down_spw(const MqMoeArgs &a, const SharedExpert &shared, int shared_mode,
                      const typename TT::storage *shared_vec, const int32_t *keeps, const typename TT::storage *act,
                      unsigned int *err, hipStream_t stream) {
-  using S = typename TT::storage;
-  const dim3 grid(ceil_div(a.hidden, Slice<SW>::kRows), a.tokens);
-  hipLaunchKernelGGL((down_combine_kernel<TT, SW, CPL, SPW>), grid, dim3(kThreads), 0, stream, act, a.down, shared,
-                     a.routes, a.scores, a.score_dtype, keeps, shared_mode, shared_vec, a.shared_gate,
-                     static_cast<S *>(a.out), a.tokens, a.slots, a.hidden, a.inter, a.group_size, a.expert_count,
-                     err);
+  if constexpr (TT::dtype == MQ_BF16 && SW == 16 && CPL <= 2 && SPW <= 3) {
+    if (a.tokens >= 2) {
+      const auto blocks = [&](uint32_t r) {
+        return static_cast<int64_t>(ceil_div(a.hidden, Slice<SW>::kRows * r)) * a.tokens;
+      };
+      if (blocks(1) <= resident_blocks<down_ptr<TT, SW, CPL, SPW, 1>>())
+        launch_down_r<TT, SW, CPL, SPW, 1>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+      else if (blocks(2) <= resident_blocks<down_ptr<TT, SW, CPL, SPW, 2>>())
+        launch_down_r<TT, SW, CPL, SPW, 2>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+      else if (blocks(4) <= resident_blocks<down_ptr<TT, SW, CPL, SPW, 4>>() || SPW == 3)
+        launch_down_r<TT, SW, CPL, SPW, 4>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+      else
+        launch_down_r<TT, SW, CPL, SPW, (SPW <= 2 ? 8 : 4)>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+      return;
+    }
+  }
+  launch_down_r<TT, SW, CPL, SPW, 1>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
 }
 
 template <class TT>

@@ -27,9 +27,9 @@ __device__ __forceinline__ uint4 ld_nt(const uint16_t *p) {
 }
 
 // bf16 dot of one 32-value chunk: products are exact in float32 (bf16 x bf16),
-// accumulated in float64.
+// accumulated in float64 in two independent chains (even and odd inputs).
 __device__ __forceinline__ double chunk_dot_f64(const uint4 *a, const uint4 *b) {
-  double acc = 0.0;
+  double acc0 = 0.0, acc1 = 0.0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const uint32_t ua[4] = {a[j].x, a[j].y, a[j].z, a[j].w};
@@ -38,17 +38,19 @@ __device__ __forceinline__ double chunk_dot_f64(const uint4 *a, const uint4 *b) 
     for (int k = 0; k < 4; ++k) {
       const float a0 = __uint_as_float(ua[k] << 16), a1 = __uint_as_float(ua[k] & 0xffff0000u);
       const float b0 = __uint_as_float(ub[k] << 16), b1 = __uint_as_float(ub[k] & 0xffff0000u);
-      acc += static_cast<double>(a0 * b0);
-      acc += static_cast<double>(a1 * b1);
+      acc0 += static_cast<double>(a0 * b0);
+      acc1 += static_cast<double>(a1 * b1);
     }
   }
-  return acc;
+  return acc0 + acc1;
 }
 
 // logits[t, e] = bf16(sum_k x[t,k] * W[e,k]) for e < routed_rows; the extra
 // row (when shared_gate_w is set) is the shared-expert gate, written to
-// shared_logit[t].  One wave per weight row (lane = 32-input chunk), all
-// tokens of the row in turn; the weight row is loaded once (non-temporal).
+// shared_logit[t].  One wave per weight row (lane = 32-input chunk); the
+// weight row is loaded once (non-temporal) and the tokens go through in
+// groups of kTokenGroup, whose activation loads, dot chains and wave sums are
+// independent of one another.
 __global__ __launch_bounds__(kThreads) void router_logits_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate_w,
     const uint16_t *__restrict__ shared_gate_w, uint16_t *__restrict__ logits,
@@ -67,21 +69,39 @@ __global__ __launch_bounds__(kThreads) void router_logits_kernel(
 #pragma unroll
     for (int q = 0; q < 4; ++q) wv[j][q] = c < chunks ? ld_nt(w + c * 32 + q * 8) : make_uint4(0, 0, 0, 0);
   }
-  for (uint32_t t = 0; t < tokens; ++t) {
-    double acc = 0.0;
+  constexpr uint32_t kTokenGroup = 4;
+  for (uint32_t t0 = 0; t0 < tokens; t0 += kTokenGroup) {
+    double acc[kTokenGroup];
+#pragma unroll
+    for (uint32_t g = 0; g < kTokenGroup; ++g) acc[g] = 0.0;
 #pragma unroll
     for (int j = 0; j < kMaxCpl; ++j) {
       const uint32_t c = lane + 64 * j;
-      if (c < chunks)
-        acc += chunk_dot_f64(wv[j], reinterpret_cast<const uint4 *>(x + static_cast<uint64_t>(t) * hidden + c * 32));
+      if (c < chunks) {
+        uint4 xv[kTokenGroup][4];
+#pragma unroll
+        for (uint32_t g = 0; g < kTokenGroup; ++g) {  // tokens past the end re-read the last one
+          const uint4 *xr = reinterpret_cast<const uint4 *>(x + static_cast<uint64_t>(min(t0 + g, tokens - 1u)) * hidden + c * 32);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) xv[g][q] = xr[q];
+        }
+#pragma unroll
+        for (uint32_t g = 0; g < kTokenGroup; ++g) acc[g] += chunk_dot_f64(wv[j], xv[g]);
+      }
     }
-    acc = wave_sum_f64_uniform(acc);
+#pragma unroll
+    for (uint32_t g = 0; g < kTokenGroup; ++g) acc[g] = wave_sum_f64_uniform(acc[g]);
     if (lane == 0) {
-      const uint16_t v = f64_to_bf16(acc);
-      if (row < routed_rows)
-        logits[static_cast<uint64_t>(t) * routed_rows + row] = v;
-      else
-        shared_logit[t] = v;
+#pragma unroll
+      for (uint32_t g = 0; g < kTokenGroup; ++g) {
+        const uint32_t t = t0 + g;
+        if (t >= tokens) break;
+        const uint16_t v = f64_to_bf16(acc[g]);
+        if (row < routed_rows)
+          logits[static_cast<uint64_t>(t) * routed_rows + row] = v;
+        else
+          shared_logit[t] = v;
+      }
     }
   }
 }

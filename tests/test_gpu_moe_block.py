@@ -151,3 +151,62 @@ def test_segmented_sorted_rows_equal_one_call(torch_mod):
     torch.cuda.synchronize()
     assert done == tokens * slots
     assert torch.equal(y_all.view(torch.int16), y_seg.view(torch.int16))
+
+
+def test_many_token_layer_rows_equal_single_token_layers(torch_mod, layer):
+    """Tokens are independent: a 16-token routed layer (one selection pass, the
+    expert kernels taking several row groups per wave, the router's token
+    groups) gives each token the bits of a 1-token layer (selection folded into
+    gate/up, one row group per wave)."""
+    torch = torch_mod
+    say("case: 16-token layer rows vs 1-token layers")
+    from flashnext_hip.moe_block import DecodeLayer
+
+    weights = layer[0]
+    for threshold in (1.0, 0.85):
+        many = DecodeLayer(weights, 16, K, threshold=threshold, min_keep=2)
+        one = DecodeLayer(weights, 1, K, threshold=threshold, min_keep=2)
+        x = to_dev_bf16(bf16_normal((16, H), seed=540))
+        many.x.copy_(x)
+        many.launch(None)
+        torch.cuda.synchronize()
+        for t in range(16):
+            one.x.copy_(x[t:t + 1])
+            one.launch(None)
+            torch.cuda.synchronize()
+            for name in ("routes", "inds", "keeps", "logits"):
+                assert torch.equal(getattr(many, name)[t:t + 1].view(-1), getattr(one, name).view(-1)), (name, t)
+            for name in ("scores", "shared_gate", "out"):
+                a, b = getattr(many, name)[t:t + 1], getattr(one, name)
+                assert torch.equal(a.reshape(-1).view(torch.int16), b.reshape(-1).view(torch.int16)), (name, t)
+
+
+def test_many_token_shared_epilogues_equal_single_token_calls(torch_mod):
+    """shared_y and shared/shared_gate epilogues at 8 tokens (several row
+    groups per down wave) against the same tokens one call at a time."""
+    torch = torch_mod
+    say("case: 8-token executor epilogues vs 1-token calls")
+    from flashnext_hip.hip_runtime import HipMoEExecutor
+
+    experts, tokens = 16, 8
+    records = make_records(experts, H, I, seed=550)
+    dev = {n: to_dev_bank(b) for n, b in (("gate_proj", records.gate), ("up_proj", records.up),
+                                           ("down_proj", records.down))}
+    rng = np.random.default_rng(551)
+    inds = np.stack([rng.choice(experts, K, replace=False) for _ in range(tokens)]).astype(np.int64)
+    raw = rng.random((tokens, K)).astype(np.float32) + 0.05
+    sc = torch.from_numpy((raw / raw.sum(1, keepdims=True)).astype(np.float32)).cuda()
+    x = to_dev_bf16(bf16_normal((tokens, H), seed=552))
+    r = torch.from_numpy(inds).cuda()
+    shared_y = to_dev_bf16(bf16_normal((tokens, H), seed=553, std=0.25))
+    shared = to_dev_bf16(bf16_normal((tokens, H), seed=554, std=0.25))
+    gate = to_dev_bf16(bf16.f32_to_bf16(rng.random((tokens, 1)).astype(np.float32)))
+    ex = HipMoEExecutor(experts, H, K, max_tokens=tokens)
+    for kw in ({}, {"shared_y": shared_y}, {"shared": shared, "shared_gate": gate}):
+        full = ex.execute(x, r, dev, scores=sc, **kw)
+        torch.cuda.synchronize()
+        for t in range(tokens):
+            kw1 = {k: v[t:t + 1] for k, v in kw.items()}
+            one = ex.execute(x[t:t + 1], r[t:t + 1], dev, scores=sc[t:t + 1], **kw1)
+            torch.cuda.synchronize()
+            assert torch.equal(full[t:t + 1].view(torch.int16), one.view(torch.int16)), (sorted(kw), t)
