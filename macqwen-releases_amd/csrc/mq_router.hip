@@ -48,9 +48,13 @@ __device__ __forceinline__ double chunk_dot_f64(const uint4 *a, const uint4 *b) 
 // logits[t, e] = bf16(sum_k x[t,k] * W[e,k]) for e < routed_rows; the extra
 // row (when shared_gate_w is set) is the shared-expert gate, written to
 // shared_logit[t].  One wave per weight row (lane = 32-input chunk); the
-// weight row is loaded once (non-temporal) and the tokens go through in
-// groups of kTokenGroup, whose activation loads, dot chains and wave sums are
-// independent of one another.
+// tokens go in groups of kTokenGroup, spread over gridDim.y blocks per row
+// (group blockIdx.y, then every gridDim.y-th).  The weight row is loaded once
+// per block (non-temporal), and a group's activation loads, dot chains and
+// wave sums are independent of one another.
+constexpr uint32_t kTokenGroup = 4;      // tokens per group
+constexpr uint32_t kMaxGroupBlocks = 64;  // blocks per weight row
+
 __global__ __launch_bounds__(kThreads) void router_logits_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate_w,
     const uint16_t *__restrict__ shared_gate_w, uint16_t *__restrict__ logits,
@@ -69,8 +73,9 @@ __global__ __launch_bounds__(kThreads) void router_logits_kernel(
 #pragma unroll
     for (int q = 0; q < 4; ++q) wv[j][q] = c < chunks ? ld_nt(w + c * 32 + q * 8) : make_uint4(0, 0, 0, 0);
   }
-  constexpr uint32_t kTokenGroup = 4;
-  for (uint32_t t0 = 0; t0 < tokens; t0 += kTokenGroup) {
+  const uint32_t groups = (tokens + kTokenGroup - 1u) / kTokenGroup;
+  for (uint32_t grp = blockIdx.y; grp < groups; grp += gridDim.y) {
+    const uint32_t t0 = grp * kTokenGroup;
     double acc[kTokenGroup];
 #pragma unroll
     for (uint32_t g = 0; g < kTokenGroup; ++g) acc[g] = 0.0;
@@ -149,7 +154,8 @@ int launch_router_logits(const uint16_t *x, const uint16_t *gate_w, const uint16
   if (hidden > 8192) return fail(MQ_ERR_UNSUPPORTED, "router hidden size %u exceeds 8192", hidden);
   const uint32_t rows = routed_rows + (shared_gate_w ? 1u : 0u);
   if (rows == 0) return MQ_OK;
-  hipLaunchKernelGGL(router_logits_kernel, dim3(ceil_div(rows, kWaves)), dim3(kThreads), 0, stream, x, gate_w,
+  const uint32_t group_blocks = std::min(ceil_div(tokens, kTokenGroup), kMaxGroupBlocks);
+  hipLaunchKernelGGL(router_logits_kernel, dim3(ceil_div(rows, kWaves), group_blocks), dim3(kThreads), 0, stream, x, gate_w,
                      shared_gate_w, logits, shared_logit, tokens, hidden, routed_rows);
   return check_launch("router_logits_kernel");
 }
