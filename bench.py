@@ -319,6 +319,90 @@ def stack_bench(torch, dev, runners, stream, steps: int = 128) -> dict:
             "router_bytes_per_token": L * EXPERTS * HIDDEN * 2}
 
 
+def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_steps: int = 2,
+                  pool_gb: float = 6.0, copy_engines: int = 4) -> dict:
+    """The 48-block stack decoded through a 6 GB LRU hot pool: per layer the
+    router runs, its experts are assigned slots on the host (hits move to the
+    LRU tail, misses evict the head), missed records are copied from pinned
+    host memory on a copy stream, and the expert kernels read the pool through
+    slot words.  One host synchronisation per layer (the route hand-off), as in
+    the reference's pool pass.  Host images are the 512 records of layer 0,
+    shared by every layer (same bytes per copy as distinct images)."""
+    import numpy as np
+
+    from flashnext_hip.layout import HEADER_SIZE
+    from flashnext_hip.moe_block import DecodeLayer, LayerWeights
+    from flashnext_hip.pool import HipExpertPool, HostRecordStore
+
+    handle = stream.cuda_stream
+    L = len(runners)
+    pool = HipExpertPool(int(pool_gb * 1e9), HIDDEN, INTER, GROUP, device=dev)
+    stride = pool.stride
+    store = HostRecordStore(pool.layout)
+    src = layers[0].pool
+    table0 = layers[0].slot_table.cpu().tolist()
+    images = []
+    for e in range(EXPERTS):
+        base = HEADER_SIZE + int(table0[e]) * stride
+        img = torch.empty(stride, dtype=torch.uint8, pin_memory=True)
+        img.copy_(src[base:base + stride])
+        images.append(img)
+    for l in range(L):
+        for e in range(EXPERTS):
+            store._records[(l, e)] = images[e]
+    table = torch.zeros(EXPERTS, dtype=torch.int32, device=dev)  # words are rewritten on the host per layer
+    dls = []
+    for r in runners:
+        w = LayerWeights(r.w.layout, pool.buffer, table, r.w.router_w, r.w.shared_gate_w, r.w.shared)
+        dls.append(DecodeLayer(w, 1, TOP_K, device=dev))
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(6)
+    xs = torch.randn((warm_steps + steps, L, 1, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
+    copy_streams = [torch.cuda.Stream() for _ in range(copy_engines)]
+    torch.cuda.synchronize()
+
+    def step(s):
+        for l, dl in enumerate(dls):
+            dl.x.copy_(xs[s, l])
+            dl.launch_router(handle)
+            inds = dl.inds.cpu()  # the route hand-off (synchronises the stream)
+            slots, misses = pool.assign(l, sorted(set(inds.reshape(-1).tolist())))
+            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copy_streams)
+            dl.routes.copy_(HipExpertPool.route_words(slots, inds).to(dev, non_blocking=False))
+            dl.launch_experts(handle)
+
+    with torch.cuda.stream(stream):
+        for s in range(warm_steps):
+            step(s)
+        torch.cuda.synchronize()
+        pool.hits = pool.misses = 0
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        wall0 = time.perf_counter()
+        start.record(stream)
+        for s in range(warm_steps, warm_steps + steps):
+            step(s)
+        end.record(stream)
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - wall0) * 1e3
+    from flashnext_hip import _lib
+
+    _lib.check_device_errors(handle)
+    ms = start.elapsed_time(end) / steps
+    misses = pool.misses / steps
+    lookups = (pool.hits + pool.misses) / steps
+    miss_bytes = misses * stride
+    out = {"workload": f"{L} stacked MoE blocks through a {pool_gb:g} GB LRU hot pool ({pool.slots} slots), "
+                       f"{steps} decode steps, fresh N(0,1) hidden per step and layer, misses copied from pinned "
+                       f"host memory on {copy_engines} copy streams",
+           "us_per_token": round(ms * 1000, 1), "wall_us_per_token": round(wall_ms * 1000 / steps, 1),
+           "slots": pool.slots, "expert_lookups_per_token": round(lookups, 1),
+           "misses_per_token": round(misses, 1), "hit_rate": round(1 - misses / lookups, 4),
+           "miss_bytes_per_token": int(miss_bytes),
+           "h2d_gbps": round(miss_bytes / (ms * 1e-3) / 1e9, 1)}
+    del dls, pool, store, images
+    return out
+
+
 def peaks_bench(torch, dev) -> dict:
     """Measured ceilings on this GPU: a 1 GiB device copy and a bf16 GEMM."""
     a = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -333,7 +417,19 @@ def peaks_bench(torch, dev) -> dict:
     end.record()
     torch.cuda.synchronize()
     copy_gbps = 2 * a.numel() * 10 / (start.elapsed_time(end) * 1e-3) / 1e9
-    del a, b
+    del b
+    h = torch.empty(256 << 20, dtype=torch.uint8, pin_memory=True)
+    d = a[:h.numel()]
+    for _ in range(2):
+        d.copy_(h, non_blocking=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(10):
+        d.copy_(h, non_blocking=True)
+    end.record()
+    torch.cuda.synchronize()
+    h2d_gbps = h.numel() * 10 / (start.elapsed_time(end) * 1e-3) / 1e9
+    del a, d, h
     n = 8192
     m1 = torch.randn((n, n), device=dev).to(torch.bfloat16)
     m2 = torch.randn((n, n), device=dev).to(torch.bfloat16)
@@ -346,8 +442,10 @@ def peaks_bench(torch, dev) -> dict:
     end.record()
     torch.cuda.synchronize()
     tflops = 2 * n ** 3 * 20 / (start.elapsed_time(end) * 1e-3) / 1e12
-    return {"copy_gbps": round(copy_gbps, 1), "bf16_gemm_tflops_8192": round(tflops, 1),
-            "note": "device-to-device copy counts read + write bytes; GEMM through torch.matmul (hipBLASLt)"}
+    return {"copy_gbps": round(copy_gbps, 1), "h2d_pinned_gbps": round(h2d_gbps, 1),
+            "bf16_gemm_tflops_8192": round(tflops, 1),
+            "note": "device-to-device copy counts read + write bytes; host-to-device from 256 MiB of pinned "
+                    "memory; GEMM through torch.matmul (hipBLASLt)"}
 
 
 def load_traffic(kernel_tag: str):
@@ -390,6 +488,7 @@ def main() -> int:
     ap.add_argument("--pmc-pass", action="store_true", help="eager launches for rocprofv3 --pmc, no timing")
     ap.add_argument("--prefill-only", action="store_true", help="time only the 4096-token prefill grouped path")
     ap.add_argument("--verify-only", action="store_true", help="time only the 4- and 16-token verify layers")
+    ap.add_argument("--hotpool-only", action="store_true", help="time only the 6 GB hot-pool stack")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the expert-parallel "
@@ -432,6 +531,10 @@ def main() -> int:
         return 0
     if args.verify_only:
         print(json.dumps({"verify": [verify_bench(torch, dev, runners, stream, t) for t in (4, 16)]}), flush=True)
+        return 0
+    if args.hotpool_only:
+        print(json.dumps({"stack_hot_pool": [hotpool_bench(torch, dev, layers, runners, stream, copy_engines=n)
+                                             for n in (1, 2, 4)]}), flush=True)
         return 0
     log("capturing graphs")
     g_all = capture(torch, lambda: [r.launch(handle) for r in runners], stream)
@@ -479,6 +582,8 @@ def main() -> int:
         log(f"verify: {extras['verify']}")
         extras["stack"] = stack_bench(torch, dev, runners, stream)
         log(f"stack: {extras['stack']}")
+        extras["stack_hot_pool"] = hotpool_bench(torch, dev, layers, runners, stream)
+        log(f"stack hot pool: {extras['stack_hot_pool']}")
         extras["peaks_measured"] = peaks_bench(torch, dev)
         log(f"peaks: {extras['peaks_measured']}")
     prefill = None

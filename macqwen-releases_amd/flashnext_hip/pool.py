@@ -114,24 +114,36 @@ class HipExpertPool:
 
         The copies run on ``copy_stream`` after everything already queued on
         ``compute_stream`` (earlier readers of the victim slots); the compute
-        stream then waits for them.  Returns the completion event.
+        stream then waits for them.  ``copy_stream`` may also be a sequence of
+        streams: the misses are split into contiguous shares, one per stream,
+        so that several DMA engines move them at once.  Returns the completion
+        events (one per copy stream) as a list, or the single event.
         """
         compute = compute_stream if compute_stream is not None else torch.cuda.current_stream(self.buffer.device)
-        copy = copy_stream if copy_stream is not None else compute
-        done = torch.cuda.Event()
-        if copy is not compute:
-            copy.wait_stream(compute)
-        n = len(misses)
-        slots = (ctypes.c_uint32 * max(n, 1))(*[int(slot) for _e, slot in misses])
+        copies = list(copy_stream) if isinstance(copy_stream, (list, tuple)) else \
+            [copy_stream if copy_stream is not None else compute]
+        misses = list(misses)
         recs = [store.record(layer, e) for e, _slot in misses]  # owned by the store: outlive the copies
-        ptrs = (ctypes.c_void_p * max(n, 1))(*[r.data_ptr() for r in recs])
-        rc = self._lib.mq_pool_refill_async(
-            ctypes.c_void_p(self.buffer.data_ptr()), HEADER_SIZE, self.stride, self.slots, slots, ptrs, n,
-            self.stride, ctypes.c_void_p(copy.cuda_stream), None)
-        _lib.check(rc, self._lib)
-        done.record(copy)
-        compute.wait_event(done)
-        return done
+        share = -(-len(misses) // len(copies)) if misses else 0
+        events = []
+        for i, copy in enumerate(copies):
+            part = misses[i * share:(i + 1) * share]
+            part_recs = recs[i * share:(i + 1) * share]
+            done = torch.cuda.Event()
+            if copy is not compute:
+                copy.wait_stream(compute)
+            n = len(part)
+            slots = (ctypes.c_uint32 * max(n, 1))(*[int(slot) for _e, slot in part])
+            ptrs = (ctypes.c_void_p * max(n, 1))(*[r.data_ptr() for r in part_recs])
+            rc = self._lib.mq_pool_refill_async(
+                ctypes.c_void_p(self.buffer.data_ptr()), HEADER_SIZE, self.stride, self.slots, slots, ptrs, n,
+                self.stride, ctypes.c_void_p(copy.cuda_stream), None)
+            _lib.check(rc, self._lib)
+            done.record(copy)
+            events.append(done)
+        for done in events:
+            compute.wait_event(done)
+        return events if isinstance(copy_stream, (list, tuple)) else events[0]
 
     # ------------------------------------------------------------ addressing
     def projection(self, name: str) -> _lib.MqProjection:
