@@ -55,6 +55,44 @@ __device__ __forceinline__ double chunk_dot_f64(const uint4 *a, const uint4 *b) 
 constexpr uint32_t kTokenGroup = 4;      // tokens per group
 constexpr uint32_t kMaxGroupBlocks = 64;  // blocks per weight row
 
+// Logits of tokens t0 .. t0 + G - 1 (all below `tokens`) for the wave's row.
+template <uint32_t G>
+__device__ __forceinline__ void row_logits(const uint4 (&wv)[4][4], const uint16_t *__restrict__ x, uint32_t t0,
+                                           uint32_t hidden, uint32_t chunks, int lane, uint32_t row,
+                                           uint32_t routed_rows, uint16_t *__restrict__ logits,
+                                           uint16_t *__restrict__ shared_logit) {
+  double acc[G];
+#pragma unroll
+  for (uint32_t g = 0; g < G; ++g) acc[g] = 0.0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t c = lane + 64 * j;
+    if (c < chunks) {
+      uint4 xv[G][4];
+#pragma unroll
+      for (uint32_t g = 0; g < G; ++g) {
+        const uint4 *xr = reinterpret_cast<const uint4 *>(x + static_cast<uint64_t>(t0 + g) * hidden + c * 32);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) xv[g][q] = xr[q];
+      }
+#pragma unroll
+      for (uint32_t g = 0; g < G; ++g) acc[g] += chunk_dot_f64(wv[j], xv[g]);
+    }
+  }
+#pragma unroll
+  for (uint32_t g = 0; g < G; ++g) acc[g] = wave_sum_f64_uniform(acc[g]);
+  if (lane == 0) {
+#pragma unroll
+    for (uint32_t g = 0; g < G; ++g) {
+      const uint16_t v = f64_to_bf16(acc[g]);
+      if (row < routed_rows)
+        logits[static_cast<uint64_t>(t0 + g) * routed_rows + row] = v;
+      else
+        shared_logit[t0 + g] = v;
+    }
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void router_logits_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate_w,
     const uint16_t *__restrict__ shared_gate_w, uint16_t *__restrict__ logits,
@@ -65,10 +103,9 @@ __global__ __launch_bounds__(kThreads) void router_logits_kernel(
   if (row >= rows) return;
   const uint16_t *w = row < routed_rows ? gate_w + static_cast<uint64_t>(row) * hidden : shared_gate_w;
   const uint32_t chunks = hidden >> 5;
-  constexpr int kMaxCpl = 4;  // hidden <= 8192
-  uint4 wv[kMaxCpl][4];
+  uint4 wv[4][4];  // hidden <= 8192: at most four 32-input chunks per lane
 #pragma unroll
-  for (int j = 0; j < kMaxCpl; ++j) {
+  for (int j = 0; j < 4; ++j) {
     const uint32_t c = lane + 64 * j;
 #pragma unroll
     for (int q = 0; q < 4; ++q) wv[j][q] = c < chunks ? ld_nt(w + c * 32 + q * 8) : make_uint4(0, 0, 0, 0);
@@ -76,37 +113,11 @@ __global__ __launch_bounds__(kThreads) void router_logits_kernel(
   const uint32_t groups = (tokens + kTokenGroup - 1u) / kTokenGroup;
   for (uint32_t grp = blockIdx.y; grp < groups; grp += gridDim.y) {
     const uint32_t t0 = grp * kTokenGroup;
-    double acc[kTokenGroup];
-#pragma unroll
-    for (uint32_t g = 0; g < kTokenGroup; ++g) acc[g] = 0.0;
-#pragma unroll
-    for (int j = 0; j < kMaxCpl; ++j) {
-      const uint32_t c = lane + 64 * j;
-      if (c < chunks) {
-        uint4 xv[kTokenGroup][4];
-#pragma unroll
-        for (uint32_t g = 0; g < kTokenGroup; ++g) {  // tokens past the end re-read the last one
-          const uint4 *xr = reinterpret_cast<const uint4 *>(x + static_cast<uint64_t>(min(t0 + g, tokens - 1u)) * hidden + c * 32);
-#pragma unroll
-          for (int q = 0; q < 4; ++q) xv[g][q] = xr[q];
-        }
-#pragma unroll
-        for (uint32_t g = 0; g < kTokenGroup; ++g) acc[g] += chunk_dot_f64(wv[j], xv[g]);
-      }
-    }
-#pragma unroll
-    for (uint32_t g = 0; g < kTokenGroup; ++g) acc[g] = wave_sum_f64_uniform(acc[g]);
-    if (lane == 0) {
-#pragma unroll
-      for (uint32_t g = 0; g < kTokenGroup; ++g) {
-        const uint32_t t = t0 + g;
-        if (t >= tokens) break;
-        const uint16_t v = f64_to_bf16(acc[g]);
-        if (row < routed_rows)
-          logits[static_cast<uint64_t>(t) * routed_rows + row] = v;
-        else
-          shared_logit[t] = v;
-      }
+    if (tokens - t0 >= kTokenGroup) {
+      row_logits<kTokenGroup>(wv, x, t0, hidden, chunks, lane, row, routed_rows, logits, shared_logit);
+    } else {  // the last 1..3 tokens one at a time (a single token pays for no idle chains)
+      for (uint32_t t = t0; t < tokens; ++t)
+        row_logits<1>(wv, x, t, hidden, chunks, lane, row, routed_rows, logits, shared_logit);
     }
   }
 }
