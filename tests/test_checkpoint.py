@@ -119,3 +119,4 @@ def test_read_layer_rejects_other_bit_widths(tmp_path):
     write_safetensors(str(tmp_path / "model.safetensors"), tensors)
     with pytest.raises(ValueError, match="4-bit"):
         read_layer(SafeTensorIndex(str(tmp_path)), 0)
+

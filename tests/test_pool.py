@@ -100,6 +100,14 @@ def test_pool_refill_bytes_and_decode_through_slots():
     torch.cuda.synchronize()
     for e, slot in misses4:
         assert torch.equal(pool.record_bytes(slot).cpu(), store.record(4, e))
+    # misses split over two copy streams land in the same places
+    store.add_banks(5, banks)
+    slots5, misses5 = pool.assign(5, [3, 8, 1, 10, 6])
+    events = pool.fill(5, misses5, store, copy_stream=[copy, torch.cuda.Stream()])
+    assert isinstance(events, list) and len(events) == 2
+    torch.cuda.synchronize()
+    for e, slot in misses5:
+        assert torch.equal(pool.record_bytes(slot).cpu(), store.record(5, e))
     with pytest.raises(ValueError):  # a slot outside the pool is rejected before any copy
         lib = _lib.load()
         import ctypes
