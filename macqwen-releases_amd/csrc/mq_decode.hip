@@ -759,31 +759,27 @@ const void *down_ptr() {
   return reinterpret_cast<const void *>(down_combine_kernel<TT, SW, CPL, SPW, R>);
 }
 
-// Down launch for SPW sources per wave.  One token keeps one row group per
-// wave (the grid of the hidden rows is resident at once).  Several tokens
-// take 2, 4 or 8 row groups per wave (bf16, 16-lane slices of at most two
-// chunks per lane, at most three sources per wave): the smallest count whose grid is resident at once,
-// so that a verify batch streams in one round of blocks instead of rounds that
-// each pay the route-word and weight latencies.
+// Down launch for SPW sources per wave.  With 16-lane slices (bf16, at most
+// two chunks per lane, at most three sources per wave) a wave takes 2, 4 or
+// 8 row groups: the smallest count of at least two whose grid is resident at
+// once, so that a verify batch streams in one round of blocks instead of
+// rounds that each pay the route-word and weight latencies (one token: two
+// row groups, measured faster than one).
 template <class TT, int SW, int CPL, int SPW>
 void launch_down_spw(const MqMoeArgs &a, const SharedExpert &shared, int shared_mode,
                      const typename TT::storage *shared_vec, const int32_t *keeps, const typename TT::storage *act,
                      unsigned int *err, hipStream_t stream) {
   if constexpr (TT::dtype == MQ_BF16 && SW == 16 && CPL <= 2 && SPW <= 3) {
-    if (a.tokens >= 2) {
-      const auto blocks = [&](uint32_t r) {
-        return static_cast<int64_t>(ceil_div(a.hidden, Slice<SW>::kRows * r)) * a.tokens;
-      };
-      if (blocks(1) <= resident_blocks<down_ptr<TT, SW, CPL, SPW, 1>>())
-        launch_down_r<TT, SW, CPL, SPW, 1>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
-      else if (blocks(2) <= resident_blocks<down_ptr<TT, SW, CPL, SPW, 2>>())
-        launch_down_r<TT, SW, CPL, SPW, 2>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
-      else if (blocks(4) <= resident_blocks<down_ptr<TT, SW, CPL, SPW, 4>>() || SPW == 3)
-        launch_down_r<TT, SW, CPL, SPW, 4>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
-      else
-        launch_down_r<TT, SW, CPL, SPW, (SPW <= 2 ? 8 : 4)>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
-      return;
-    }
+    const auto blocks = [&](uint32_t r) {
+      return static_cast<int64_t>(ceil_div(a.hidden, Slice<SW>::kRows * r)) * a.tokens;
+    };
+    if (blocks(2) <= resident_blocks<down_ptr<TT, SW, CPL, SPW, 2>>())
+      launch_down_r<TT, SW, CPL, SPW, 2>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+    else if (blocks(4) <= resident_blocks<down_ptr<TT, SW, CPL, SPW, 4>>() || SPW == 3)
+      launch_down_r<TT, SW, CPL, SPW, 4>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+    else
+      launch_down_r<TT, SW, CPL, SPW, (SPW <= 2 ? 8 : 4)>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
+    return;
   }
   launch_down_r<TT, SW, CPL, SPW, 1>(a, shared, shared_mode, shared_vec, keeps, act, err, stream);
 }
