@@ -93,12 +93,14 @@ __device__ __forceinline__ void row_logits(const uint4 (&wv)[4][4], const uint16
   }
 }
 
-__global__ __launch_bounds__(kThreads) void router_logits_kernel(
+constexpr uint32_t kLogitsWaves = 1;  // one weight row per block: the rows spread over every CU
+
+__global__ __launch_bounds__(64 * kLogitsWaves) void router_logits_kernel(
     const uint16_t *__restrict__ x, const uint16_t *__restrict__ gate_w,
     const uint16_t *__restrict__ shared_gate_w, uint16_t *__restrict__ logits,
     uint16_t *__restrict__ shared_logit, uint32_t tokens, uint32_t hidden, uint32_t routed_rows) {
   const int lane = threadIdx.x & 63;
-  const uint32_t row = blockIdx.x * kWaves + (threadIdx.x >> 6);
+  const uint32_t row = blockIdx.x * kLogitsWaves + (threadIdx.x >> 6);
   const uint32_t rows = routed_rows + (shared_gate_w ? 1u : 0u);
   if (row >= rows) return;
   const uint16_t *w = row < routed_rows ? gate_w + static_cast<uint64_t>(row) * hidden : shared_gate_w;
@@ -166,8 +168,8 @@ int launch_router_logits(const uint16_t *x, const uint16_t *gate_w, const uint16
   const uint32_t rows = routed_rows + (shared_gate_w ? 1u : 0u);
   if (rows == 0) return MQ_OK;
   const uint32_t group_blocks = std::min(ceil_div(tokens, kTokenGroup), kMaxGroupBlocks);
-  hipLaunchKernelGGL(router_logits_kernel, dim3(ceil_div(rows, kWaves), group_blocks), dim3(kThreads), 0, stream, x, gate_w,
-                     shared_gate_w, logits, shared_logit, tokens, hidden, routed_rows);
+  hipLaunchKernelGGL(router_logits_kernel, dim3(ceil_div(rows, kLogitsWaves), group_blocks), dim3(64 * kLogitsWaves), 0,
+                     stream, x, gate_w, shared_gate_w, logits, shared_logit, tokens, hidden, routed_rows);
   return check_launch("router_logits_kernel");
 }
 
