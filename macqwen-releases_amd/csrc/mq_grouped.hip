@@ -214,6 +214,75 @@ __global__ void grouped_scatter_kernel(const uint32_t *__restrict__ row_key, uin
   if (active) order[pos] = r;
 }
 
+// Block-histogram variants for key spaces that fit in LDS (kLdsKeys).  Each
+// block takes kSortRows consecutive rows and counts them in an LDS histogram
+// first, so a hot expert costs one global atomic per block instead of one
+// per wave (Zipf-skewed prefill routes put thousands of rows on one key, and
+// same-address global atomics serialize).
+constexpr uint32_t kSortThreads = 256;
+constexpr uint32_t kSortPerThread = 8;
+constexpr uint32_t kSortRows = kSortThreads * kSortPerThread;
+constexpr uint32_t kLdsKeys = 16384;  // 64 KB of dynamic LDS
+
+__global__ __launch_bounds__(kSortThreads) void grouped_count_lds_kernel(
+    const uint32_t *__restrict__ routes, uint32_t routed_rows, uint32_t rows, KeySpace ks,
+    uint32_t *__restrict__ counts, uint32_t *__restrict__ row_key, unsigned int *__restrict__ err) {
+  extern __shared__ uint32_t hist[];
+  const uint32_t nk = ks.size();
+  for (uint32_t i = threadIdx.x; i < nk; i += kSortThreads) hist[i] = 0u;
+  __syncthreads();
+  const uint32_t base = blockIdx.x * kSortRows;
+  bool bad = false;
+#pragma unroll
+  for (uint32_t j = 0; j < kSortPerThread; ++j) {
+    const uint32_t r = base + j * kSortThreads + threadIdx.x;
+    if (r < rows) {
+      const uint32_t key = r < routed_rows ? key_of(routes[r], ks) : ks.shared_key();
+      bad |= key == ks.dead_key();
+      row_key[r] = key;
+      atomicAdd(&hist[key], 1u);
+    }
+  }
+  if (__ballot(bad) != 0ull && (threadIdx.x & 63) == 0) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < nk; i += kSortThreads) {
+    const uint32_t c = hist[i];
+    if (c != 0u) atomicAdd(&counts[i], c);
+  }
+}
+
+// Scatter: each row's position is its key's cursor, advanced once per block
+// by the block's count of that key, plus the row's rank among the block's
+// rows of that key (the LDS atomic's return value).
+__global__ __launch_bounds__(kSortThreads) void grouped_scatter_lds_kernel(const uint32_t *__restrict__ row_key,
+                                                                          uint32_t rows, KeySpace ks,
+                                                                          uint32_t *__restrict__ cursor,
+                                                                          uint32_t *__restrict__ order) {
+  extern __shared__ uint32_t hist[];
+  const uint32_t nk = ks.size();
+  for (uint32_t i = threadIdx.x; i < nk; i += kSortThreads) hist[i] = 0u;
+  __syncthreads();
+  const uint32_t base = blockIdx.x * kSortRows;
+  uint32_t key[kSortPerThread], rank[kSortPerThread];
+#pragma unroll
+  for (uint32_t j = 0; j < kSortPerThread; ++j) {
+    const uint32_t r = base + j * kSortThreads + threadIdx.x;
+    key[j] = r < rows ? row_key[r] : 0u;
+    rank[j] = r < rows ? atomicAdd(&hist[key[j]], 1u) : 0u;
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < nk; i += kSortThreads) {
+    const uint32_t c = hist[i];
+    if (c != 0u) hist[i] = atomicAdd(&cursor[i], c);
+  }
+  __syncthreads();
+#pragma unroll
+  for (uint32_t j = 0; j < kSortPerThread; ++j) {
+    const uint32_t r = base + j * kSortThreads + threadIdx.x;
+    if (r < rows) order[hist[key[j]] + rank[j]] = r;
+  }
+}
+
 // ------------------------------------------------------------------ GEMM
 template <int B>
 __device__ __forceinline__ float ubyte_to_f32(uint32_t v) {
@@ -312,17 +381,27 @@ __device__ __forceinline__ void store_xstage(uint16_t *xb, const XStage &r, uint
     *reinterpret_cast<uint4 *>(xb + xs_off(xrow, kXChunks * xpart + j)) = r.x[j];
 }
 
+// The B operand of slab t at k16 step j: tile row 32 t + lane%32, eight
+// inputs at 64 h + 8 j of the stage (`xl` is the lane's base in the LDS
+// activation tile).
+__device__ __forceinline__ bf16x8_t b_frag(const uint16_t *xl, int t, int j) {
+  return *reinterpret_cast<const bf16x8_t *>(xl + 32u * t * kXRow + 8u * j);
+}
+
 // One k16 step: C[32 weight rows x 32 tile rows] += A . B for the NSLAB
-// active slabs (the tile's rows, 32 per slab), with `xl` the lane's base in
-// the LDS activation tile (row lane%32, inputs 64 h) and j the step within
-// the stage.  The slab count is a template argument so that no branch splits
-// the MFMA stream.
+// active slabs (the tile's rows, 32 per slab).  The B fragments of step j
+// were read during step j - 1; each slab's register is refilled with step
+// j + 1 as soon as its MFMA has issued, so an LDS read has a whole step
+// (the next A dequantization and the other slabs' MFMAs) to land instead of
+// stalling the MFMA that follows it.  The slab count is a template argument
+// so that no branch splits the MFMA stream.
 template <int NSLAB>
-__device__ __forceinline__ void mma_step(f32x16_t (&acc)[4], const uint16_t *xl, const bf16x8_t &a, int j) {
+__device__ __forceinline__ void mma_step(f32x16_t (&acc)[4], bf16x8_t (&bq)[4], const uint16_t *xl,
+                                         const bf16x8_t &a, int j) {
 #pragma unroll
   for (int t = 0; t < NSLAB; ++t) {
-    const bf16x8_t b = *reinterpret_cast<const bf16x8_t *>(xl + 32u * t * kXRow + 8u * j);
-    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[t], 0, 0, 0);
+    acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[t], acc[t], 0, 0, 0);
+    if (j < 7) bq[t] = b_frag(xl, t, j + 1);
   }
 }
 
@@ -350,6 +429,9 @@ __device__ __forceinline__ void stage_mma(f32x16_t (&acc)[4], const uint16_t *xl
   // dequantized while the MFMAs of step j run; a scheduling barrier per step
   // keeps the compiler from hoisting further ahead (which only adds live
   // registers: the other wave on the SIMD covers the LDS latency).
+  bf16x8_t bq[4];
+#pragma unroll
+  for (int t = 0; t < NSLAB; ++t) bq[t] = b_frag(xl, t, 0);
   bf16x8_t a = dequant_word(w.w[0].x, s0, b0);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -362,7 +444,7 @@ __device__ __forceinline__ void stage_mma(f32x16_t (&acc)[4], const uint16_t *xl
     }
     if (j == 3) w.w[0] = buf_load16(lw.e.w, off_w);  // words 0-3 consumed
     if (j == 7) w.w[1] = buf_load16(lw.e.w, off_w + 16u);
-    mma_step<NSLAB>(acc, xl, a, j);
+    mma_step<NSLAB>(acc, bq, xl, a, j);
     a = an;
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -746,9 +828,11 @@ int validate_proj_grouped(const MqProjection &p, const char *name) {
   return MQ_OK;
 }
 
-// Weight stages in flight: a divisor of the stages per item (3..5 where one
-// divides it), so the ring slot of a stage is fixed and the load cursor
-// stays within one item of the compute cursor.
+// Weight stages in flight: a divisor of the stages per item, so the ring
+// slot of a stage is fixed and the load cursor stays within one item of the
+// compute cursor.  Two stages ahead keep the kernel within 256 registers per
+// lane with the B-fragment read-ahead (four stages spill; measured on the
+// 4096-token chunk: 4 stages 918-928 us, 2 stages 897-909 us per call).
 template <bool DOWN, int NS>
 int launch_gemm_ns(const GemmParams &p, uint32_t group, uint32_t grid, hipStream_t s) {
   if (group == 32)
@@ -761,10 +845,8 @@ int launch_gemm_ns(const GemmParams &p, uint32_t group, uint32_t grid, hipStream
 template <bool DOWN>
 int launch_gemm(const GemmParams &p, uint32_t group, uint32_t grid, hipStream_t s) {
   const uint32_t stages = p.K / kKS;
-  if (stages % 4 == 0) return launch_gemm_ns<DOWN, 4>(p, group, grid, s);
-  if (stages % 5 == 0) return launch_gemm_ns<DOWN, 5>(p, group, grid, s);
-  if (stages % 3 == 0) return launch_gemm_ns<DOWN, 3>(p, group, grid, s);
   if (stages % 2 == 0) return launch_gemm_ns<DOWN, 2>(p, group, grid, s);
+  if (stages % 3 == 0) return launch_gemm_ns<DOWN, 3>(p, group, grid, s);
   return launch_gemm_ns<DOWN, 1>(p, group, grid, s);
 }
 
@@ -833,13 +915,23 @@ extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
 
   hipLaunchKernelGGL(grouped_zero_kernel, dim3(ceil_div(ks.size(), 256)), dim3(256), 0, s, counts, ks.size());
   if ((rc = check_launch("grouped_zero_kernel"))) return rc;
-  hipLaunchKernelGGL(grouped_count_kernel, dim3(ceil_div(l.rows, 256)), dim3(256), 0, s, a.routes, routed_rows,
-                     l.rows, ks, counts, row_key, err);
+  const bool lds_sort = ks.size() <= kLdsKeys;
+  const uint32_t hist_bytes = ks.size() * 4u;
+  if (lds_sort)
+    hipLaunchKernelGGL(grouped_count_lds_kernel, dim3(ceil_div(l.rows, kSortRows)), dim3(kSortThreads), hist_bytes, s,
+                       a.routes, routed_rows, l.rows, ks, counts, row_key, err);
+  else
+    hipLaunchKernelGGL(grouped_count_kernel, dim3(ceil_div(l.rows, 256)), dim3(256), 0, s, a.routes, routed_rows,
+                       l.rows, ks, counts, row_key, err);
   if ((rc = check_launch("grouped_count_kernel"))) return rc;
   hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, counts, cursor, tiles, n_tiles, ks);
   if ((rc = check_launch("grouped_plan_kernel"))) return rc;
-  hipLaunchKernelGGL(grouped_scatter_kernel, dim3(ceil_div(l.rows, 256)), dim3(256), 0, s, row_key, l.rows, cursor,
-                     order);
+  if (lds_sort)
+    hipLaunchKernelGGL(grouped_scatter_lds_kernel, dim3(ceil_div(l.rows, kSortRows)), dim3(kSortThreads), hist_bytes,
+                       s, row_key, l.rows, ks, cursor, order);
+  else
+    hipLaunchKernelGGL(grouped_scatter_kernel, dim3(ceil_div(l.rows, 256)), dim3(256), 0, s, row_key, l.rows, cursor,
+                       order);
   if ((rc = check_launch("grouped_scatter_kernel"))) return rc;
 
   int device = 0, cus = 0;
