@@ -11,12 +11,14 @@
 //   1. count / plan / scatter: a counting sort of the rows by route key (pool
 //      slot or expert id; the shared expert is one more key over all tokens)
 //      and a tile list of (route word, first sorted row, rows <= 128);
-//   2. gate/up GEMM: per (tile, 64 features) a 256-thread block stages the
-//      tile's token rows of x and the 128 weight rows (64 gate + 64 up
-//      features) dequantized to bf16 in LDS, 64 inputs per stage, and runs
-//      v_mfma_f32_32x32x16_bf16 (fp32 accumulate); the epilogue rounds gate
-//      and up to bf16 and writes act = swiglu(g, u) in sorted row order;
-//   3. down GEMM: per (tile, 128 features) the same scheme over act, the
+//   2. gate/up GEMM: a persistent grid of 8-wave blocks (one per CU) walks
+//      (tile, 128 features) items.  Each wave streams 32 weight rows (waves
+//      0-3 gate, 4-7 up) straight into registers, dequantizes them to bf16
+//      MFMA operands there, and multiplies them with the tile's token rows,
+//      staged 128 inputs per stage in LDS, on v_mfma_f32_32x32x16_bf16
+//      (fp32 accumulate); the epilogue rounds gate and up to bf16 and writes
+//      act = swiglu(g, u) in sorted row order;
+//   3. down GEMM: per (tile, 256 features) the same scheme over act, the
 //      bf16 outputs are scattered back to y[token, slot] (or the shared
 //      expert's row);
 //   4. combine: out = bf16 generic combine of y with the scores + the gated
@@ -657,7 +659,7 @@ struct Pipe {
       for (int u = 0; u < NS; ++u) {
         const uint32_t s = s0 + u;
         uint16_t *xb = xs + (s & 1u) * kXTile;
-        store_xstage(xb, xv, xrow, xpart);
+        if (xrow < 32u * NSLAB) store_xstage(xb, xv, xrow, xpart);  // rows past the active slabs are never read
         __syncthreads();
         const bool last = u == NS - 1 && s + 1u == S;
         if (last) xsrc_next = x_source<DOWN>(n, p, tid);

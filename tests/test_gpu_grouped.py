@@ -127,6 +127,46 @@ def test_grouped_heavy_expert_many_tiles_and_pool_words(torch_mod):
     assert torch.equal(out_d.view(torch.int16), out_p.view(torch.int16))
 
 
+def test_grouped_large_pool_key_space_matches_dense(torch_mod):
+    """A pool of 16,400 slots puts the route-key space past what the block
+    histograms hold in LDS (16,384 keys), so the count and scatter take the
+    wave-aggregated global-atomic kernels; the bits must equal the dense call,
+    which sorts through LDS histograms."""
+    torch = torch_mod
+    say("case: grouped large pool key space (global-atomic sort)")
+    from flashnext_hip import _lib
+    from flashnext_hip.grouped import GroupedMoE
+    from flashnext_hip.layout import make_layout
+    from flashnext_hip.moe_block import pool_projection
+
+    tokens, slots, experts, hidden, inter = 300, 6, 10, 128, 128
+    records = make_records(experts, hidden, inter, seed=340)
+    x = bf16_normal((tokens, hidden), seed=341)
+    inds, scores = _zipf_routes(tokens, slots, experts, seed=342)
+    dense = GroupedMoE(*_banks(records, torch), hidden=hidden, inter=inter)
+    out_d, y_d = dense(to_dev_bf16(x), torch.from_numpy(inds.astype(np.int32)).cuda(), to_dev_bf16(scores))
+    torch.cuda.synchronize()
+    want_out, want_y = moe.prefill_layer(x, inds, scores, records, weights="bf16")
+    exact_out, exact_y = moe.prefill_layer(x, inds, scores, records)
+    _check(from_dev_bf16(y_d), want_y, exact_y, "small-shape y")
+    _check(from_dev_bf16(out_d), want_out, exact_out, "small-shape out")
+
+    pool_slots = 16400
+    rng = np.random.default_rng(343)
+    perm = np.concatenate([[pool_slots - 1, 16384], rng.choice(np.arange(16390), size=experts - 2, replace=False)])
+    img, _ = pool_from_banks(records, perm, pool_slots, hidden, inter)
+    pool_t = torch.from_numpy(img).cuda()
+    del img
+    lay = make_layout(hidden, inter)
+    projs = [pool_projection(pool_t, lay, n) for n in ("gate_proj", "up_proj", "down_proj")]
+    pooled = GroupedMoE(*projs, hidden=hidden, inter=inter)
+    words = (np.uint64(_lib.MQ_SLOT_BIT) | perm[inds].astype(np.uint64)).astype(np.uint32).view(np.int32)
+    out_p, y_p = pooled(to_dev_bf16(x), torch.from_numpy(words).cuda(), to_dev_bf16(scores))
+    torch.cuda.synchronize()
+    assert torch.equal(y_d.view(torch.int16), y_p.view(torch.int16))
+    assert torch.equal(out_d.view(torch.int16), out_p.view(torch.int16))
+
+
 def test_grouped_invalid_route_word_flags_and_zeroes(torch_mod):
     torch = torch_mod
     say("case: grouped invalid route word")
