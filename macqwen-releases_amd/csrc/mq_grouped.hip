@@ -10,7 +10,8 @@
 // Here:
 //   1. count / plan / scatter: a counting sort of the rows by route key (pool
 //      slot or expert id; the shared expert is one more key over all tokens)
-//      and a tile list of (route word, first sorted row, rows <= 128);
+//      and a tile list of (route word, first sorted row, rows <= 128), in one
+//      block up to 40,960 rows and 12,288 keys, else in four kernels;
 //   2. gate/up GEMM: a persistent grid of 8-wave blocks (one per CU) walks
 //      (tile, 128 features) items.  Each wave streams 32 weight rows (waves
 //      0-3 gate, 4-7 up) straight into registers, dequantizes them to bf16
@@ -161,12 +162,12 @@ __global__ void grouped_count_kernel(const uint32_t *__restrict__ routes, uint32
 }
 
 // One block: exclusive scans of the rows and tiles per key, the scatter
-// cursors, and the tile list.  Each thread owns a contiguous run of keys.
-__global__ __launch_bounds__(kPlanThreads) void grouped_plan_kernel(const uint32_t *__restrict__ counts,
-                                                                     uint32_t *__restrict__ cursor,
-                                                                     GroupTile *__restrict__ tiles,
-                                                                     uint32_t *__restrict__ n_tiles, KeySpace ks) {
-  __shared__ uint32_t s_rows[kPlanThreads], s_tiles[kPlanThreads];
+// cursors, and the tile list.  Each thread owns a contiguous run of keys and
+// reads each key's count before it writes that key's cursor, so `counts` and
+// `cursor` may be the same array (the single-block sort keeps both in LDS).
+__device__ __forceinline__ void plan_keys(const uint32_t *counts, uint32_t *cursor, GroupTile *__restrict__ tiles,
+                                          uint32_t *__restrict__ n_tiles, KeySpace ks, uint32_t *s_rows,
+                                          uint32_t *s_tiles) {
   const uint32_t keys = ks.size();
   const uint32_t per = (keys + kPlanThreads - 1) / kPlanThreads;
   const uint32_t lo = min(threadIdx.x * per, keys), hi = min(lo + per, keys);
@@ -205,6 +206,64 @@ __global__ __launch_bounds__(kPlanThreads) void grouped_plan_kernel(const uint32
     row_off += c;
   }
   if (threadIdx.x == kPlanThreads - 1) *n_tiles = s_tiles[kPlanThreads - 1];
+}
+
+__global__ __launch_bounds__(kPlanThreads) void grouped_plan_kernel(const uint32_t *__restrict__ counts,
+                                                                     uint32_t *__restrict__ cursor,
+                                                                     GroupTile *__restrict__ tiles,
+                                                                     uint32_t *__restrict__ n_tiles, KeySpace ks) {
+  __shared__ uint32_t s_rows[kPlanThreads], s_tiles[kPlanThreads];
+  plan_keys(counts, cursor, tiles, n_tiles, ks, s_rows, s_tiles);
+}
+
+// The whole sort in one block when the rows fit in registers (KPT <= 40 keys
+// per thread, two 16-bit keys per register) and the key histogram in LDS: count into the LDS histogram, scan it
+// in place into the cursors and the tile list, then scatter through LDS
+// atomics.  One launch instead of four (zero, count, plan, scatter), which is
+// most of the sort's cost at verify and small-prefill row counts.
+constexpr uint32_t kSingleSortKeys = 12288;  // 48 KB of dynamic LDS beside the 8 KB of scan scratch
+
+template <int KPT>
+__global__ __launch_bounds__(kPlanThreads) void grouped_sort_single_kernel(
+    const uint32_t *__restrict__ routes, uint32_t routed_rows, uint32_t rows, KeySpace ks,
+    uint32_t *__restrict__ order, GroupTile *__restrict__ tiles, uint32_t *__restrict__ n_tiles,
+    unsigned int *__restrict__ err) {
+  constexpr int kBatch = KPT < 16 ? KPT : (KPT % 16 == 0 ? 16 : 8);  // route loads in flight per thread
+  static_assert(KPT % kBatch == 0 && kBatch % 2 == 0 && kSingleSortKeys <= 65536u, "16-bit keys");
+  extern __shared__ uint32_t hist[];
+  __shared__ uint32_t s_rows[kPlanThreads], s_tiles[kPlanThreads];
+  const uint32_t nk = ks.size();
+  for (uint32_t i = threadIdx.x; i < nk; i += kPlanThreads) hist[i] = 0u;
+  uint32_t kp[KPT / 2];  // row (j * 1024 + tid)'s key in bits 16 (j & 1) .. +15 of kp[j / 2]
+  bool bad = false;
+  __syncthreads();  // the histogram is zero
+#pragma unroll
+  for (int b = 0; b < KPT; b += kBatch) {
+    uint32_t w[kBatch];
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const uint32_t r = static_cast<uint32_t>(b + i) * kPlanThreads + threadIdx.x;
+      w[i] = r < routed_rows ? routes[r] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const uint32_t r = static_cast<uint32_t>(b + i) * kPlanThreads + threadIdx.x;
+      const uint32_t key = r < rows ? (r < routed_rows ? key_of(w[i], ks) : ks.shared_key()) : 0u;
+      bad |= r < rows && key == ks.dead_key();
+      if (r < rows) atomicAdd(&hist[key], 1u);
+      if (i & 1) kp[(b + i) / 2] |= key << 16;
+      else kp[(b + i) / 2] = key;
+    }
+  }
+  if (__ballot(bad) != 0ull && (threadIdx.x & 63) == 0) raise_flag(err, MQ_DEVFLAG_BAD_ROUTE);
+  __syncthreads();
+  plan_keys(hist, hist, tiles, n_tiles, ks, s_rows, s_tiles);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < KPT; ++j) {
+    const uint32_t r = static_cast<uint32_t>(j) * kPlanThreads + threadIdx.x;
+    if (r < rows) order[atomicAdd(&hist[(kp[j / 2] >> (16 * (j & 1))) & 0xffffu], 1u)] = r;
+  }
 }
 
 __global__ void grouped_scatter_kernel(const uint32_t *__restrict__ row_key, uint32_t rows,
@@ -915,26 +974,41 @@ extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
   uint16_t *y_shared = shared_expert ? reinterpret_cast<uint16_t *>(ws + l.y_shared) : nullptr;
   const uint32_t routed_rows = a.tokens * a.slots;
 
-  hipLaunchKernelGGL(grouped_zero_kernel, dim3(ceil_div(ks.size(), 256)), dim3(256), 0, s, counts, ks.size());
-  if ((rc = check_launch("grouped_zero_kernel"))) return rc;
-  const bool lds_sort = ks.size() <= kLdsKeys;
-  const uint32_t hist_bytes = ks.size() * 4u;
-  if (lds_sort)
-    hipLaunchKernelGGL(grouped_count_lds_kernel, dim3(ceil_div(l.rows, kSortRows)), dim3(kSortThreads), hist_bytes, s,
-                       a.routes, routed_rows, l.rows, ks, counts, row_key, err);
-  else
-    hipLaunchKernelGGL(grouped_count_kernel, dim3(ceil_div(l.rows, 256)), dim3(256), 0, s, a.routes, routed_rows,
-                       l.rows, ks, counts, row_key, err);
-  if ((rc = check_launch("grouped_count_kernel"))) return rc;
-  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, counts, cursor, tiles, n_tiles, ks);
-  if ((rc = check_launch("grouped_plan_kernel"))) return rc;
-  if (lds_sort)
-    hipLaunchKernelGGL(grouped_scatter_lds_kernel, dim3(ceil_div(l.rows, kSortRows)), dim3(kSortThreads), hist_bytes,
-                       s, row_key, l.rows, ks, cursor, order);
-  else
-    hipLaunchKernelGGL(grouped_scatter_kernel, dim3(ceil_div(l.rows, 256)), dim3(256), 0, s, row_key, l.rows, cursor,
-                       order);
-  if ((rc = check_launch("grouped_scatter_kernel"))) return rc;
+  if (ks.size() <= kSingleSortKeys && l.rows <= 40u * kPlanThreads) {
+    const uint32_t kpt = ceil_div(l.rows, kPlanThreads);
+    const uint32_t hist_bytes = ks.size() * 4u;
+    if (kpt <= 4)
+      hipLaunchKernelGGL(grouped_sort_single_kernel<4>, dim3(1), dim3(kPlanThreads), hist_bytes, s, a.routes,
+                         routed_rows, l.rows, ks, order, tiles, n_tiles, err);
+    else if (kpt <= 16)
+      hipLaunchKernelGGL(grouped_sort_single_kernel<16>, dim3(1), dim3(kPlanThreads), hist_bytes, s, a.routes,
+                         routed_rows, l.rows, ks, order, tiles, n_tiles, err);
+    else
+      hipLaunchKernelGGL(grouped_sort_single_kernel<40>, dim3(1), dim3(kPlanThreads), hist_bytes, s, a.routes,
+                         routed_rows, l.rows, ks, order, tiles, n_tiles, err);
+    if ((rc = check_launch("grouped_sort_single_kernel"))) return rc;
+  } else {
+    hipLaunchKernelGGL(grouped_zero_kernel, dim3(ceil_div(ks.size(), 256)), dim3(256), 0, s, counts, ks.size());
+    if ((rc = check_launch("grouped_zero_kernel"))) return rc;
+    const bool lds_sort = ks.size() <= kLdsKeys;
+    const uint32_t hist_bytes = ks.size() * 4u;
+    if (lds_sort)
+      hipLaunchKernelGGL(grouped_count_lds_kernel, dim3(ceil_div(l.rows, kSortRows)), dim3(kSortThreads), hist_bytes, s,
+                         a.routes, routed_rows, l.rows, ks, counts, row_key, err);
+    else
+      hipLaunchKernelGGL(grouped_count_kernel, dim3(ceil_div(l.rows, 256)), dim3(256), 0, s, a.routes, routed_rows,
+                         l.rows, ks, counts, row_key, err);
+    if ((rc = check_launch("grouped_count_kernel"))) return rc;
+    hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, counts, cursor, tiles, n_tiles, ks);
+    if ((rc = check_launch("grouped_plan_kernel"))) return rc;
+    if (lds_sort)
+      hipLaunchKernelGGL(grouped_scatter_lds_kernel, dim3(ceil_div(l.rows, kSortRows)), dim3(kSortThreads), hist_bytes,
+                         s, row_key, l.rows, ks, cursor, order);
+    else
+      hipLaunchKernelGGL(grouped_scatter_kernel, dim3(ceil_div(l.rows, 256)), dim3(256), 0, s, row_key, l.rows, cursor,
+                         order);
+    if ((rc = check_launch("grouped_scatter_kernel"))) return rc;
+  }
 
   int device = 0, cus = 0;
   MQ_TRY_HIP(hipGetDevice(&device));

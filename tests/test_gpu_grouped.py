@@ -127,13 +127,14 @@ def test_grouped_heavy_expert_many_tiles_and_pool_words(torch_mod):
     assert torch.equal(out_d.view(torch.int16), out_p.view(torch.int16))
 
 
-def test_grouped_large_pool_key_space_matches_dense(torch_mod):
-    """A pool of 16,400 slots puts the route-key space past what the block
-    histograms hold in LDS (16,384 keys), so the count and scatter take the
-    wave-aggregated global-atomic kernels; the bits must equal the dense call,
-    which sorts through LDS histograms."""
+@pytest.mark.parametrize("pool_slots", [13000, 16400])
+def test_grouped_large_pool_key_space_matches_dense(torch_mod, pool_slots):
+    """Pools past the single-block sort's 12,288 keys: 13,000 slots sort with
+    multi-block LDS histograms, 16,400 (past 16,384 keys) with wave-aggregated
+    global atomics.  The bits must equal the dense call, which sorts in one
+    block."""
     torch = torch_mod
-    say("case: grouped large pool key space (global-atomic sort)")
+    say(f"case: grouped large pool key space ({pool_slots} slots)")
     from flashnext_hip import _lib
     from flashnext_hip.grouped import GroupedMoE
     from flashnext_hip.layout import make_layout
@@ -151,9 +152,8 @@ def test_grouped_large_pool_key_space_matches_dense(torch_mod):
     _check(from_dev_bf16(y_d), want_y, exact_y, "small-shape y")
     _check(from_dev_bf16(out_d), want_out, exact_out, "small-shape out")
 
-    pool_slots = 16400
     rng = np.random.default_rng(343)
-    perm = np.concatenate([[pool_slots - 1, 16384], rng.choice(np.arange(16390), size=experts - 2, replace=False)])
+    perm = np.concatenate([[pool_slots - 1, 12300], rng.choice(np.arange(12290), size=experts - 2, replace=False)])
     img, _ = pool_from_banks(records, perm, pool_slots, hidden, inter)
     pool_t = torch.from_numpy(img).cuda()
     del img
@@ -165,6 +165,26 @@ def test_grouped_large_pool_key_space_matches_dense(torch_mod):
     torch.cuda.synchronize()
     assert torch.equal(y_d.view(torch.int16), y_p.view(torch.int16))
     assert torch.equal(out_d.view(torch.int16), out_p.view(torch.int16))
+
+
+def test_grouped_many_rows_multi_block_sort(torch_mod):
+    """42,000 (token, slot) rows: past the single-block sort's 40,960, so the
+    rows are counted and scattered by multi-block LDS histograms."""
+    torch = torch_mod
+    say("case: grouped 4200 tokens x 10 slots (multi-block sort)")
+    from flashnext_hip.grouped import GroupedMoE
+
+    tokens, slots, experts, hidden, inter = 4200, 10, 24, 128, 128
+    records = make_records(experts, hidden, inter, seed=350)
+    x = bf16_normal((tokens, hidden), seed=351)
+    inds, scores = _zipf_routes(tokens, slots, experts, seed=352)
+    want_out, want_y = moe.prefill_layer(x, inds, scores, records, weights="bf16")
+    exact_out, exact_y = moe.prefill_layer(x, inds, scores, records)
+    g = GroupedMoE(*_banks(records, torch), hidden=hidden, inter=inter)
+    out, y = g(to_dev_bf16(x), torch.from_numpy(inds.astype(np.int32)).cuda(), to_dev_bf16(scores))
+    torch.cuda.synchronize()
+    _check(from_dev_bf16(y), want_y, exact_y, "many-row y")
+    _check(from_dev_bf16(out), want_out, exact_out, "many-row out")
 
 
 def test_grouped_invalid_route_word_flags_and_zeroes(torch_mod):
