@@ -363,10 +363,12 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 // K order inside a stage.  MFMA k-slots can be assigned to inputs in any
 // order as long as both operands agree.  Lane l (fragment row or tile row
 // l%32, half h = l/32) supplies, at k16-step j of a stage, the eight inputs
-// k0 + 64 h + 8 j .. +7: each lane then owns 64 consecutive inputs of its
-// row per stage, i.e. 32 contiguous bytes of packed weights (two 16-byte
-// loads straight into registers, no LDS), and the same 128 contiguous bytes
-// of its activation row.
+// k0 + 32 h + 8 j .. +7 for j < 4 and k0 + 64 + 32 h + 8 (j - 4) .. +7 for
+// j >= 4.  A lane's packed weights are then two 16-byte pieces (words 4h ..
+// 4h+3 and 8+4h .. 8+4h+3 of the row's 64-byte stage), loaded straight into
+// registers with no LDS, and lanes l and l + 32 read adjacent pieces, so
+// each load instruction reads 32 contiguous bytes of each of the wave's 32
+// rows.  The activation fragments follow the same order.
 
 // Activation tile in LDS: 128 rows x 128 bf16, rows padded by one 16-byte
 // chunk (272 bytes), so the 32 rows of a slab read at one chunk column fall
@@ -390,9 +392,8 @@ __device__ __forceinline__ bf16x8_t dequant_word(uint32_t w, float s, float b) {
 constexpr uint32_t kXTile = kTileRows * kXRow;  // bf16 per LDS activation tile
 
 // One lane's weights for one stage: 64 inputs of its weight row as 8 packed
-// words (two 16-byte loads) and the scales and biases of their groups.  Group
-// 32: two bf16 in one 32-bit load (words 0-3 use the low half, words 4-7 the
-// high half); group 64: one bf16 for all eight words.
+// words (two 16-byte loads) and the scales and biases of their groups as bf16
+// pairs (words 0-3 use the low half, words 4-7 the high half).
 struct WStage {
   uint4 w[2];
   uint32_t s, b;
@@ -407,20 +408,41 @@ struct WRow {
   bool ok;
 };
 
+// Byte offset of a lane's first weight piece of a stage: lanes l and l + 32
+// (halves 0 and 1) read adjacent 16-byte pieces, so each of the two load
+// instructions reads 32 contiguous bytes of each of the wave's 32 rows.
+__device__ __forceinline__ uint32_t wstage_off(const WRow &wr, uint32_t K, uint32_t stage, uint32_t half) {
+  return wr.ok ? wr.row * (K / 2u) + stage * (kKS / 2u) + 16u * half : kOutOfRange;
+}
+
+// Group scales and biases of a lane's words, as bf16 pairs: the low half for
+// w[0], the high half for w[1].  Group 32: groups half and half + 2 of the
+// stage's four; group 64: groups 0 and 1.
+template <int G>
+__device__ __forceinline__ void load_groups(uint32_t &s, uint32_t &b, const WRow &wr, uint32_t K, uint32_t stage,
+                                            uint32_t half) {
+  const uint32_t g0 = wr.row * (K / G) + stage * (kKS / G);
+  if constexpr (G == 32) {  // the stage's four groups in one 8-byte load, then (g[half], g[half + 2])
+    const uint32_t o = wr.ok ? g0 * 2u : kOutOfRange;
+    typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t sv = __builtin_amdgcn_raw_buffer_load_b64(wr.e.s, static_cast<int>(o), 0, 0);
+    const u32x2_t bv = __builtin_amdgcn_raw_buffer_load_b64(wr.e.b, static_cast<int>(o), 0, 0);
+    const uint32_t sel = half ? 0x07060302u : 0x05040100u;
+    s = __builtin_amdgcn_perm(sv.y, sv.x, sel);
+    b = __builtin_amdgcn_perm(bv.y, bv.x, sel);
+  } else {
+    const uint32_t o = wr.ok ? g0 * 2u : kOutOfRange;
+    s = buf_load4(wr.e.s, o);
+    b = buf_load4(wr.e.b, o);
+  }
+}
+
 template <int G>
 __device__ __forceinline__ void load_wstage(WStage &r, const WRow &wr, uint32_t K, uint32_t stage, uint32_t half) {
-  const uint32_t k0 = stage * kKS + 64u * half;
-  const uint32_t off_w = wr.ok ? wr.row * (K / 2u) + k0 / 2u : kOutOfRange;
-  const uint32_t off_g = wr.ok ? (wr.row * (K / G) + k0 / G) * 2u : kOutOfRange;
+  const uint32_t off_w = wstage_off(wr, K, stage, half);
   r.w[0] = buf_load16(wr.e.w, off_w);
-  r.w[1] = buf_load16(wr.e.w, off_w + 16u);
-  if constexpr (G == 32) {
-    r.s = buf_load4(wr.e.s, off_g);
-    r.b = buf_load4(wr.e.b, off_g);
-  } else {
-    r.s = buf_load2(wr.e.s, off_g);
-    r.b = buf_load2(wr.e.b, off_g);
-  }
+  r.w[1] = buf_load16(wr.e.w, off_w + 32u);
+  load_groups<G>(r.s, r.b, wr, K, stage, half);
 }
 
 // A thread's share of the activation tile of one stage: kXChunks 16-byte
@@ -443,10 +465,10 @@ __device__ __forceinline__ void store_xstage(uint16_t *xb, const XStage &r, uint
 }
 
 // The B operand of slab t at k16 step j: tile row 32 t + lane%32, eight
-// inputs at 64 h + 8 j of the stage (`xl` is the lane's base in the LDS
-// activation tile).
+// inputs at 32 h + 8 j (+ 32 for j >= 4) of the stage (`xl` is the lane's
+// base in the LDS activation tile, at input 32 h).
 __device__ __forceinline__ bf16x8_t b_frag(const uint16_t *xl, int t, int j) {
-  return *reinterpret_cast<const bf16x8_t *>(xl + 32u * t * kXRow + 8u * j);
+  return *reinterpret_cast<const bf16x8_t *>(xl + 32u * t * kXRow + 8u * j + (j >= 4 ? 32u : 0u));
 }
 
 // One k16 step: C[32 weight rows x 32 tile rows] += A . B for the NSLAB
@@ -474,18 +496,9 @@ template <int G, int NSLAB>
 __device__ __forceinline__ void stage_mma(f32x16_t (&acc)[4], const uint16_t *xl, WStage &w, const WRow &lw,
                                           uint32_t K, uint32_t ls, uint32_t half) {
   const float s0 = __uint_as_float(w.s << 16), b0 = __uint_as_float(w.b << 16);
-  const float s1 = G == 32 ? __uint_as_float(w.s & 0xffff0000u) : s0;
-  const float b1 = G == 32 ? __uint_as_float(w.b & 0xffff0000u) : b0;
-  const uint32_t k0 = ls * kKS + 64u * half;
-  const uint32_t off_w = lw.ok ? lw.row * (K / 2u) + k0 / 2u : kOutOfRange;
-  const uint32_t off_g = lw.ok ? (lw.row * (K / G) + k0 / G) * 2u : kOutOfRange;
-  if constexpr (G == 32) {
-    w.s = buf_load4(lw.e.s, off_g);
-    w.b = buf_load4(lw.e.b, off_g);
-  } else {
-    w.s = buf_load2(lw.e.s, off_g);
-    w.b = buf_load2(lw.e.b, off_g);
-  }
+  const float s1 = __uint_as_float(w.s & 0xffff0000u), b1 = __uint_as_float(w.b & 0xffff0000u);
+  const uint32_t off_w = wstage_off(lw, K, ls, half);
+  load_groups<G>(w.s, w.b, lw, K, ls, half);
   // Software pipeline over the eight k16 steps: the A operand of step j+1 is
   // dequantized while the MFMAs of step j run; a scheduling barrier per step
   // keeps the compiler from hoisting further ahead (which only adds live
@@ -504,7 +517,7 @@ __device__ __forceinline__ void stage_mma(f32x16_t (&acc)[4], const uint16_t *xl
       an = dequant_word(word, k < 4 ? s0 : s1, k < 4 ? b0 : b1);
     }
     if (j == 3) w.w[0] = buf_load16(lw.e.w, off_w);  // words 0-3 consumed
-    if (j == 7) w.w[1] = buf_load16(lw.e.w, off_w + 16u);
+    if (j == 7) w.w[1] = buf_load16(lw.e.w, off_w + 32u);
     mma_step<NSLAB>(acc, bq, xl, a, j);
     a = an;
     __builtin_amdgcn_sched_barrier(0);
@@ -712,7 +725,7 @@ struct Pipe {
                                       int lane, int tid, uint32_t S, __amdgpu_buffer_rsrc_t xr) {
     const uint32_t half = static_cast<uint32_t>(lane) >> 5;
     const uint32_t xrow = static_cast<uint32_t>(tid) / kXParts, xpart = static_cast<uint32_t>(tid) % kXParts;
-    const uint32_t xl_off = (static_cast<uint32_t>(lane) & 31u) * kXRow + 64u * half;
+    const uint32_t xl_off = (static_cast<uint32_t>(lane) & 31u) * kXRow + 32u * half;
     for (uint32_t s0 = 0; s0 < S; s0 += NS) {
 #pragma unroll
       for (int u = 0; u < NS; ++u) {
