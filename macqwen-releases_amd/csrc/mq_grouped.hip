@@ -11,7 +11,7 @@
 //   1. count / plan / scatter: a counting sort of the rows by route key (pool
 //      slot or expert id; the shared expert is one more key over all tokens)
 //      and a tile list of (route word, first sorted row, rows <= 128), in one
-//      block up to 40,960 rows and 12,288 keys, else in four kernels;
+//      block up to 16,384 rows and 12,288 keys, else in four kernels;
 //   2. gate/up GEMM: a persistent grid of 8-wave blocks (one per CU) walks
 //      (tile, 128 features) items.  Each wave streams 32 weight rows (waves
 //      0-3 gate, 4-7 up) straight into registers, dequantizes them to bf16
@@ -216,11 +216,12 @@ __global__ __launch_bounds__(kPlanThreads) void grouped_plan_kernel(const uint32
   plan_keys(counts, cursor, tiles, n_tiles, ks, s_rows, s_tiles);
 }
 
-// The whole sort in one block when the rows fit in registers (KPT <= 40 keys
+// The whole sort in one block when the rows fit in registers (KPT <= 16 keys
 // per thread, two 16-bit keys per register) and the key histogram in LDS: count into the LDS histogram, scan it
 // in place into the cursors and the tile list, then scatter through LDS
 // atomics.  One launch instead of four (zero, count, plan, scatter), which is
-// most of the sort's cost at verify and small-prefill row counts.
+// most of the sort's cost at verify and small-prefill row counts; at 40,960
+// rows one CU is slower (31.6 us) than the four kernels (23.5 us).
 constexpr uint32_t kSingleSortKeys = 12288;  // 48 KB of dynamic LDS beside the 8 KB of scan scratch
 
 template <int KPT>
@@ -987,17 +988,14 @@ extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
   uint16_t *y_shared = shared_expert ? reinterpret_cast<uint16_t *>(ws + l.y_shared) : nullptr;
   const uint32_t routed_rows = a.tokens * a.slots;
 
-  if (ks.size() <= kSingleSortKeys && l.rows <= 40u * kPlanThreads) {
+  if (ks.size() <= kSingleSortKeys && l.rows <= 16u * kPlanThreads) {
     const uint32_t kpt = ceil_div(l.rows, kPlanThreads);
     const uint32_t hist_bytes = ks.size() * 4u;
     if (kpt <= 4)
       hipLaunchKernelGGL(grouped_sort_single_kernel<4>, dim3(1), dim3(kPlanThreads), hist_bytes, s, a.routes,
                          routed_rows, l.rows, ks, order, tiles, n_tiles, err);
-    else if (kpt <= 16)
-      hipLaunchKernelGGL(grouped_sort_single_kernel<16>, dim3(1), dim3(kPlanThreads), hist_bytes, s, a.routes,
-                         routed_rows, l.rows, ks, order, tiles, n_tiles, err);
     else
-      hipLaunchKernelGGL(grouped_sort_single_kernel<40>, dim3(1), dim3(kPlanThreads), hist_bytes, s, a.routes,
+      hipLaunchKernelGGL(grouped_sort_single_kernel<16>, dim3(1), dim3(kPlanThreads), hist_bytes, s, a.routes,
                          routed_rows, l.rows, ks, order, tiles, n_tiles, err);
     if ((rc = check_launch("grouped_sort_single_kernel"))) return rc;
   } else {

@@ -168,7 +168,7 @@ def test_grouped_large_pool_key_space_matches_dense(torch_mod, pool_slots):
 
 
 def test_grouped_many_rows_multi_block_sort(torch_mod):
-    """42,000 (token, slot) rows: past the single-block sort's 40,960, so the
+    """42,000 (token, slot) rows: past the single-block sort's 16,384, so the
     rows are counted and scattered by multi-block LDS histograms."""
     torch = torch_mod
     say("case: grouped 4200 tokens x 10 slots (multi-block sort)")
