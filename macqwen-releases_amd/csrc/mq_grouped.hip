@@ -49,6 +49,7 @@ constexpr int kPlanThreads = 1024;
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t2 __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
 struct GroupTile {
   uint32_t word;   // route word of the group (kSharedWord / kDeadWord for the extra groups)
@@ -217,9 +218,9 @@ __global__ __launch_bounds__(kPlanThreads) void grouped_plan_kernel(const uint32
 }
 
 // The whole sort in one block when the rows fit in registers (KPT <= 16 keys
-// per thread, two 16-bit keys per register) and the key histogram in LDS: count into the LDS histogram, scan it
-// in place into the cursors and the tile list, then scatter through LDS
-// atomics.  One launch instead of four (zero, count, plan, scatter), which is
+// per thread, two 16-bit keys per register) and the key histogram in LDS:
+// count into the LDS histogram, scan it in place into the cursors and the
+// tile list, then scatter through LDS atomics.  One launch instead of four (zero, count, plan, scatter), which is
 // most of the sort's cost at verify and small-prefill row counts; at 40,960
 // rows one CU is slower (31.6 us) than the four kernels (23.5 us).
 constexpr uint32_t kSingleSortKeys = 12288;  // 48 KB of dynamic LDS beside the 8 KB of scan scratch
@@ -229,7 +230,7 @@ __global__ __launch_bounds__(kPlanThreads) void grouped_sort_single_kernel(
     const uint32_t *__restrict__ routes, uint32_t routed_rows, uint32_t rows, KeySpace ks,
     uint32_t *__restrict__ order, GroupTile *__restrict__ tiles, uint32_t *__restrict__ n_tiles,
     unsigned int *__restrict__ err) {
-  constexpr int kBatch = KPT < 16 ? KPT : (KPT % 16 == 0 ? 16 : 8);  // route loads in flight per thread
+  constexpr int kBatch = KPT < 16 ? KPT : 16;  // route loads in flight per thread
   static_assert(KPT % kBatch == 0 && kBatch % 2 == 0 && kSingleSortKeys <= 65536u, "16-bit keys");
   extern __shared__ uint32_t hist[];
   __shared__ uint32_t s_rows[kPlanThreads], s_tiles[kPlanThreads];
@@ -425,7 +426,6 @@ __device__ __forceinline__ void load_groups(uint32_t &s, uint32_t &b, const WRow
   const uint32_t g0 = wr.row * (K / G) + stage * (kKS / G);
   if constexpr (G == 32) {  // the stage's four groups in one 8-byte load, then (g[half], g[half + 2])
     const uint32_t o = wr.ok ? g0 * 2u : kOutOfRange;
-    typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
     const u32x2_t sv = __builtin_amdgcn_raw_buffer_load_b64(wr.e.s, static_cast<int>(o), 0, 0);
     const u32x2_t bv = __builtin_amdgcn_raw_buffer_load_b64(wr.e.b, static_cast<int>(o), 0, 0);
     const uint32_t sel = half ? 0x07060302u : 0x05040100u;
