@@ -637,52 +637,70 @@ __device__ __forceinline__ WRow weight_row(const Item &m, const GemmParams &p, c
   return r;
 }
 
-// Gate/up epilogue: act = swiglu(bf16(g), bf16(u)) in sorted row order.  The
-// up waves hand their bf16 results to the gate waves through LDS (the tile
-// buffer just consumed); lane l of up wave 4+f holds exactly the (row,
-// feature) cells of lane l of gate wave f.
+// Gate/up epilogue: act = swiglu(bf16(g), bf16(u)) in sorted row order.  Lane
+// l of gate wave f and lane l of up wave 4+f hold the same (row, feature)
+// cells, in four runs q of 4 consecutive features.  Gate waves compute runs
+// 0-1 and up waves runs 2-3, each handing the other its bf16 values of the
+// runs the other computes through LDS (the tile buffer just consumed), so all
+// eight waves share the SwiGLU sequence.
 constexpr uint32_t kExchange = 4u * 4u * 64u * 4u;  // bf16 per gate/up wave pair: 4 slabs x 16 values x 64 lanes
 static_assert(kExchange * (kGemmWaves / 2) <= kXTile, "gate/up exchange must fit in one activation tile");
+
+__device__ __forceinline__ uint32_t ex_off(int t, int i, int lane) {  // run i (0, 1) of slab t, lane `lane`
+  return ((2u * t + i) * 64u + lane) * 4u;
+}
+
+template <bool UP>
+__device__ __forceinline__ void gateup_epilogue_half(const f32x16_t (&acc)[4], uint16_t *ex, const Item &m,
+                                                     const GemmParams &p, uint32_t nb, uint32_t fw, int lane,
+                                                     const bool (&slab)[4]) {
+  constexpr int kRun = UP ? 2 : 0;   // first run this wave computes
+  constexpr int kGive = UP ? 0 : 2;  // first run this wave hands over
+  uint16_t *give = ex + (UP ? kExchange / 2 : 0u);
+  const uint16_t *take = ex + (UP ? 0u : kExchange / 2);
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    if (slab[t])
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int q = kGive + i;
+        const uint32_t lo = f32_to_bf16(acc[t][4 * q]) | (static_cast<uint32_t>(f32_to_bf16(acc[t][4 * q + 1])) << 16);
+        const uint32_t hi =
+            f32_to_bf16(acc[t][4 * q + 2]) | (static_cast<uint32_t>(f32_to_bf16(acc[t][4 * q + 3])) << 16);
+        *reinterpret_cast<uint2 *>(give + ex_off(t, i, lane)) = make_uint2(lo, hi);
+      }
+  __syncthreads();
+  const uint32_t start = uniform(m.tile.y), count = uniform(m.tile.z);
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t trow = 32u * t + (static_cast<uint32_t>(lane) & 31u);
+    if (!slab[t] || trow >= count) continue;
+    uint16_t *dst = p.out + static_cast<uint64_t>(start + trow) * p.N;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int q = kRun + i;
+      const uint32_t feat = nb * kGateUpFeatures + 32u * fw + c_row(4 * q, lane);
+      const uint2 o = *reinterpret_cast<const uint2 *>(take + ex_off(t, i, lane));
+      const uint32_t oo[2] = {o.x, o.y};
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float own = round_bf16(acc[t][4 * q + e]);
+        const float other = __uint_as_float((e & 1) ? (oo[e >> 1] & 0xffff0000u) : (oo[e >> 1] << 16));
+        v[e] = UP ? swiglu_bf16(other, own) : swiglu_bf16(own, other);
+      }
+      if (feat < p.N) *reinterpret_cast<uint2 *>(dst + feat) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
+    }
+  }
+}
 
 __device__ __forceinline__ void gateup_epilogue(const f32x16_t (&acc)[4], uint16_t *xb, const Item &m,
                                                 const GemmParams &p, uint32_t nb, uint32_t wave, int lane,
                                                 const bool (&slab)[4]) {
   const uint32_t fw = wave % (kGemmWaves / 2);
-  uint16_t *ex = xb + fw * kExchange;
   __syncthreads();  // every wave is done reading the tile in xb
-  if (wave >= kGemmWaves / 2) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-      if (slab[t])
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          *reinterpret_cast<uint2 *>(ex + ((4u * t + q) * 64u + lane) * 4u) =
-              make_uint2(pack_bf16(acc[t][4 * q], acc[t][4 * q + 1]), pack_bf16(acc[t][4 * q + 2], acc[t][4 * q + 3]));
-  }
-  __syncthreads();
-  if (wave < kGemmWaves / 2) {
-    const uint32_t start = uniform(m.tile.y), count = uniform(m.tile.z);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint32_t trow = 32u * t + (static_cast<uint32_t>(lane) & 31u);
-      if (!slab[t] || trow >= count) continue;
-      uint16_t *dst = p.out + static_cast<uint64_t>(start + trow) * p.N;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {  // four runs of 4 consecutive features
-        const uint32_t feat = nb * kGateUpFeatures + 32u * fw + c_row(4 * q, lane);
-        const uint2 u = *reinterpret_cast<const uint2 *>(ex + ((4u * t + q) * 64u + lane) * 4u);
-        const uint32_t uu[2] = {u.x, u.y};
-        float v[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float g = round_bf16(acc[t][4 * q + e]);
-          const float up = __uint_as_float((e & 1) ? (uu[e >> 1] & 0xffff0000u) : (uu[e >> 1] << 16));
-          v[e] = swiglu_bf16(g, up);
-        }
-        if (feat < p.N) *reinterpret_cast<uint2 *>(dst + feat) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
-      }
-    }
-  }
+  if (wave >= kGemmWaves / 2) gateup_epilogue_half<true>(acc, xb + fw * kExchange, m, p, nb, fw, lane, slab);
+  else gateup_epilogue_half<false>(acc, xb + fw * kExchange, m, p, nb, fw, lane, slab);
 }
 
 // Down epilogue: the bf16 outputs go back to y[token, slot] (or the shared
