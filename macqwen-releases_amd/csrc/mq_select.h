@@ -51,11 +51,17 @@ __device__ __forceinline__ float exp_bf16(float m) {
 }
 
 // MLX bf16 sigmoid sequence (each step rounded to bf16, float32 exp correctly rounded).
+// bf16(1 / d) takes the hardware reciprocal (within 1 float32 ulp) instead of a
+// correctly rounded division: d is a bf16 value >= 2, so d = D * 2^k with D < 256;
+// unless D is a power of two (then 1/d is exact either way), the odd part D' >= 3
+// of D puts 1/d at a relative distance >= 2^-8 / D' > 2^-16 from every bf16
+// rounding midpoint (an odd multiple of 2^-9 times a power of two), far beyond
+// 2^-23, so both round to the same bf16.  d = inf gives 0 either way.
 __device__ __forceinline__ float sigmoid_bf16(float g) {
   const float m = fabsf(g);
   const float e = exp_bf16(m);
   const float d = round_bf16(__fadd_rn(1.0f, e));
-  const float s = round_bf16(__fdiv_rn(1.0f, d));
+  const float s = round_bf16(__builtin_amdgcn_rcpf(d));
   const float om = round_bf16(__fsub_rn(1.0f, s));
   return g < 0.0f ? s : om;
 }
