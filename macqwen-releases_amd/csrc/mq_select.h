@@ -38,6 +38,14 @@ __device__ __forceinline__ float badd(float a, float b) { return round_bf16(__fa
 __device__ __forceinline__ float bmul(float a, float b) { return round_bf16(__fmul_rn(a, b)); }
 __device__ __forceinline__ float bdiv(float a, float b) { return round_bf16(__fdiv_rn(a, b)); }
 
+// bf16 round-to-nearest-even in one v_cvt_pk_bf16_f32.  Equal to round_bf16
+// for every non-NaN float32, denormals and infinities included (checked over
+// all 2^32 bit patterns on gfx950); only NaN payloads may differ, so it is used
+// inside the sequences below, whose stored results are rounded again.
+__device__ __forceinline__ float round_bf16_hw(float f) {
+  return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<__bf16>(f))) << 16);
+}
+
 // bf16(exp(m)) where exp is the correctly rounded float32 exponential.
 // expf is within 2 float32 ulps of exp(m); its bf16 rounding can only differ
 // from that of the correctly rounded value when the float32 result lies
@@ -47,7 +55,7 @@ __device__ __forceinline__ float exp_bf16(float m) {
   const float e = expf(m);
   const int low = static_cast<int>(__float_as_uint(e) & 0xffffu);
   if (abs(low - 0x8000) <= 4 || !isfinite(e)) return round_bf16(static_cast<float>(exp(static_cast<double>(m))));
-  return round_bf16(e);
+  return round_bf16_hw(e);
 }
 
 // MLX bf16 sigmoid sequence (each step rounded to bf16, float32 exp correctly rounded).
@@ -60,16 +68,16 @@ __device__ __forceinline__ float exp_bf16(float m) {
 __device__ __forceinline__ float sigmoid_bf16(float g) {
   const float m = fabsf(g);
   const float e = exp_bf16(m);
-  const float d = round_bf16(__fadd_rn(1.0f, e));
-  const float s = round_bf16(__builtin_amdgcn_rcpf(d));
-  const float om = round_bf16(__fsub_rn(1.0f, s));
+  const float d = round_bf16_hw(__fadd_rn(1.0f, e));
+  const float s = round_bf16_hw(__builtin_amdgcn_rcpf(d));
+  const float om = round_bf16_hw(__fsub_rn(1.0f, s));
   return g < 0.0f ? s : om;
 }
 
 // bf16 SwiGLU of bf16-valued g and u: bf16(bf16(g * sigmoid_bf16(g)) * u)
 // (models/flashnext/metal_runtime.py:278-287).
 __device__ __forceinline__ float swiglu_bf16(float g, float u) {
-  const float silu = round_bf16(__fmul_rn(g, sigmoid_bf16(g)));
+  const float silu = round_bf16_hw(__fmul_rn(g, sigmoid_bf16(g)));
   return round_bf16(__fmul_rn(silu, u));
 }
 
