@@ -682,13 +682,15 @@ __device__ __forceinline__ void gateup_epilogue_half(const f32x16_t (&acc)[4], u
       const uint32_t feat = nb * kGateUpFeatures + 32u * fw + c_row(4 * q, lane);
       const uint2 o = *reinterpret_cast<const uint2 *>(take + ex_off(t, i, lane));
       const uint32_t oo[2] = {o.x, o.y};
-      float v[4];
+      float gv[4], uv[4], v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float own = round_bf16(acc[t][4 * q + e]);
         const float other = __uint_as_float((e & 1) ? (oo[e >> 1] & 0xffff0000u) : (oo[e >> 1] << 16));
-        v[e] = UP ? swiglu_bf16(other, own) : swiglu_bf16(own, other);
+        gv[e] = UP ? other : own;
+        uv[e] = UP ? own : other;
       }
+      swiglu_bf16_n<4>(gv, uv, v);
       if (feat < p.N) *reinterpret_cast<uint2 *>(dst + feat) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
     }
   }

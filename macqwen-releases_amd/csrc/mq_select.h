@@ -81,6 +81,36 @@ __device__ __forceinline__ float swiglu_bf16(float g, float u) {
   return round_bf16(__fmul_rn(silu, u));
 }
 
+// swiglu_bf16 of N values at once, bit for bit: the float32 exponentials are
+// taken together and the rare float64 re-evaluation runs behind one
+// wave-uniform branch, so the N sequences stay free of divergent control flow
+// and interleave.
+template <int N>
+__device__ __forceinline__ void swiglu_bf16_n(const float (&g)[N], const float (&u)[N], float (&out)[N]) {
+  float e[N];
+  uint32_t redo = 0u;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float ef = expf(fabsf(g[i]));
+    const int low = static_cast<int>(__float_as_uint(ef) & 0xffffu);
+    if (abs(low - 0x8000) <= 4 || !isfinite(ef)) redo |= 1u << i;
+    e[i] = round_bf16_hw(ef);
+  }
+  if (__ballot(redo != 0u) != 0ull) {
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if ((redo >> i) & 1u) e[i] = round_bf16(static_cast<float>(exp(static_cast<double>(fabsf(g[i])))));
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float d = round_bf16_hw(__fadd_rn(1.0f, e[i]));
+    const float s = round_bf16_hw(__builtin_amdgcn_rcpf(d));
+    const float om = round_bf16_hw(__fsub_rn(1.0f, s));
+    const float silu = round_bf16_hw(__fmul_rn(g[i], g[i] < 0.0f ? s : om));
+    out[i] = round_bf16(__fmul_rn(silu, u[i]));
+  }
+}
+
 struct SelectParams {
   const uint16_t *logits;      // [tokens, experts] bf16
   const uint32_t *slot_table;  // [experts] or nullptr
