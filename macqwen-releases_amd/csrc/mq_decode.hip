@@ -234,24 +234,26 @@ __device__ __forceinline__ float row_partial(const RowLoad<CPL> &r, const XLane<
 // exponential correctly rounded (evaluated in double).
 template <class TT>
 __device__ __forceinline__ float sigmoid_t(float g) {
-  const float m = fabsf(g);
-  float e;
-  if constexpr (TT::dtype == MQ_BF16)
-    e = exp_bf16(m);  // guarded float32 exp, float64 only near a bf16 midpoint
-  else
-    e = static_cast<float>(exp(static_cast<double>(m)));
-  const float d = TT::round(__fadd_rn(1.0f, e));
-  const float s = TT::round(__fdiv_rn(1.0f, d));
-  const float om = TT::round(__fsub_rn(1.0f, s));
-  return g < 0.0f ? s : om;
+  if constexpr (TT::dtype == MQ_BF16) {
+    return sigmoid_bf16(g);  // the bf16 sequence (guarded float32 exp), shared with the grouped path
+  } else {
+    const float e = static_cast<float>(exp(static_cast<double>(fabsf(g))));
+    const float d = TT::round(__fadd_rn(1.0f, e));
+    const float s = TT::round(__fdiv_rn(1.0f, d));
+    const float om = TT::round(__fsub_rn(1.0f, s));
+    return g < 0.0f ? s : om;
+  }
 }
 
 // act = T(T(g * sigmoid_T(g)) * u) for T-valued g and u.
 template <class TT>
 __device__ __forceinline__ float swiglu_t(float g, float u) {
-  const float sig = sigmoid_t<TT>(g);
-  const float silu = TT::round(__fmul_rn(g, sig));
-  return TT::round(__fmul_rn(silu, u));
+  if constexpr (TT::dtype == MQ_BF16) {
+    return swiglu_bf16(g, u);
+  } else {
+    const float silu = TT::round(__fmul_rn(g, sigmoid_t<TT>(g)));
+    return TT::round(__fmul_rn(silu, u));
+  }
 }
 
 // ------------------------------------------------------------------ kernels
