@@ -455,7 +455,11 @@ def load_traffic(kernel_tag: str):
         return None
     for line in path.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
-            return int(float(line.split(":", 1)[1].strip()))
+            fields = line.split(":", 1)[1].split()
+            try:
+                return int(float(fields[0]))
+            except (IndexError, ValueError):
+                return None
     return None
 
 
