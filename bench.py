@@ -190,12 +190,58 @@ def prefill_bench(torch, dev, reps: int = 10) -> dict:
     import numpy as np
 
     counts = np.bincount(inds.reshape(-1), minlength=EXPERTS)
+    out, y = g(x, routes, scores)
+    check = prefill_check(torch, banks, x, inds, scores, out, y, counts)
     del banks, g
     return {"workload": f"{T} tokens x top-{TOP_K}, {EXPERTS} experts, Zipf(1.1) rows "
                         f"(max {int(counts.max())}, median {int(np.median(counts))}, min {int(counts.min())})",
             "us": round(ms * 1000, 1), "gflop": round(flops / 1e9, 1), "tflops": round(tflops, 1),
             "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-            "note": "sort + grouped MFMA GEMMs + bf16 combine timed together; routed experts only"}
+            "note": "sort + grouped MFMA GEMMs + bf16 combine timed together; routed experts only",
+            "check": check}
+
+
+def prefill_check(torch, banks, x, inds, scores, out, y, counts) -> dict:
+    """Oracle check of the prefill chunk after timing: every row of the two
+    heaviest and two lightest experts, and the combined rows of 16 random
+    tokens (bf16-tile weights, the MFMA operands; float64 accumulation)."""
+    import numpy as np
+
+    from oracle import bf16, moe, q4
+
+    T = x.shape[0]
+    order = np.argsort(counts, kind="stable")
+    rng = np.random.default_rng(17)
+    tokens = np.sort(rng.choice(T, 16, replace=False))
+    inds_np = inds.reshape(T, TOP_K)
+    experts = sorted(set(order[-2:].tolist()) | set(order[:2].tolist()) | set(inds_np[tokens].reshape(-1).tolist()))
+    sel = torch.tensor(experts, device=x.device)
+    host = [q4.ExpertBank(b.weight[sel].cpu().numpy().view(np.uint32),
+                          b.scales[sel].view(torch.int16).cpu().numpy().view(np.uint16),
+                          b.biases[sel].view(torch.int16).cpu().numpy().view(np.uint16), GROUP) for b in banks]
+    remap = {e: i for i, e in enumerate(experts)}
+    xb = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    xf = bf16.bf16_to_f32(xb)
+    yb = y.view(torch.int16).cpu().numpy().view(np.uint16).reshape(T * TOP_K, HIDDEN)
+    flat = inds_np.reshape(-1)
+    got_rows, want_rows = [], []
+    for e in list(order[-2:]) + list(order[:2]):
+        rows = np.nonzero(flat == e)[0]
+        want_rows.append(moe.expert_mlp(xf[rows // TOP_K], host, remap[int(e)], "bf16", "bf16")[3])
+        got_rows.append(yb[rows])
+    sub = inds_np[tokens]
+    y_want = np.zeros((tokens.size, TOP_K, HIDDEN), dtype=np.uint16)
+    for e in np.unique(sub):
+        ti, si = np.nonzero(sub == e)
+        y_want[ti, si] = moe.expert_mlp(xf[tokens[ti]], host, remap[int(e)], "bf16", "bf16")[3]
+    sc = scores.view(torch.int16).cpu().numpy().view(np.uint16)[tokens]
+    want_out = bf16.bf16_to_f32(moe.generic_combine(y_want, sc))
+    got_out = bf16.bf16_to_f32(out.view(torch.int16).cpu().numpy().view(np.uint16)[tokens])
+    got = np.concatenate([bf16.bf16_to_f32(r).ravel() for r in got_rows] + [got_out.ravel()]).astype(np.float64)
+    want = np.concatenate([bf16.bf16_to_f32(r).ravel() for r in want_rows] + [want_out.ravel()]).astype(np.float64)
+    return {"rows_checked": int(sum(r.shape[0] for r in got_rows)), "tokens_checked": int(tokens.size),
+            "max_rel": float(np.abs(got - want).max() / np.abs(want).max()),
+            "cosine": float(np.dot(got, want) / (np.linalg.norm(got) * np.linalg.norm(want)))}
 
 
 def qmv_bench(torch, dev, lib, stream, copies: int = 64, reps: int = 50) -> dict:
@@ -387,9 +433,31 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
     from flashnext_hip import _lib
 
     _lib.check_device_errors(handle)
+    hits_timed, misses_timed = pool.hits, pool.misses
+    # Untimed check: one more step in which every layer also runs fully
+    # resident on the same token; the hot-pool output must be bit-identical.
+    # The resident twin of layer l has layer l's router and shared expert and
+    # layer 0's routed experts, like the host images above.
+    twins = [DecodeLayer(LayerWeights(r.w.layout, layers[0].pool, layers[0].slot_table, r.w.router_w,
+                                      r.w.shared_gate_w, r.w.shared), 1, TOP_K, device=dev) for r in runners]
+    identical = 0
+    with torch.cuda.stream(stream):
+        for l, dl in enumerate(dls):
+            twins[l].x.copy_(xs[0, l])
+            twins[l].launch(handle)
+            dl.x.copy_(xs[0, l])
+            dl.launch_router(handle)
+            inds = dl.inds.cpu()
+            slots, misses = pool.assign(l, sorted(set(inds.reshape(-1).tolist())))
+            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copy_streams)
+            dl.routes.copy_(HipExpertPool.route_words(slots, inds).to(dev, non_blocking=False))
+            dl.launch_experts(handle)
+            torch.cuda.synchronize()
+            identical += int(torch.equal(twins[l].out.view(torch.int16), dl.out.view(torch.int16)))
+    _lib.check_device_errors(handle)
     ms = start.elapsed_time(end) / steps
-    misses = pool.misses / steps
-    lookups = (pool.hits + pool.misses) / steps
+    misses = misses_timed / steps
+    lookups = (hits_timed + misses_timed) / steps
     miss_bytes = misses * stride
     out = {"workload": f"{L} stacked MoE blocks through a {pool_gb:g} GB LRU hot pool ({pool.slots} slots), "
                        f"{steps} decode steps, fresh N(0,1) hidden per step and layer, misses copied from pinned "
@@ -398,8 +466,9 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
            "slots": pool.slots, "expert_lookups_per_token": round(lookups, 1),
            "misses_per_token": round(misses, 1), "hit_rate": round(1 - misses / lookups, 4),
            "miss_bytes_per_token": int(miss_bytes),
-           "h2d_gbps": round(miss_bytes / (ms * 1e-3) / 1e9, 1)}
-    del dls, pool, store, images
+           "h2d_gbps": round(miss_bytes / (ms * 1e-3) / 1e9, 1),
+           "check": {"layers_bit_identical_to_resident": identical, "layers": L}}
+    del dls, pool, store, images, twins
     return out
 
 
@@ -541,29 +610,42 @@ def main() -> int:
                                              for n in (1, 2, 4)]}), flush=True)
         return 0
     log("capturing graphs")
+    # Step i decodes one token through layer i mod L.  The timed K steps (and
+    # the W warmup steps) are whole graph replays: K // L replays of the
+    # L-step graph, then one graph of the first K mod L layer steps.
     g_all = capture(torch, lambda: [r.launch(handle) for r in runners], stream)
     g_exp = capture(torch, lambda: [r.launch_experts(handle) for r in runners], stream)
     g_unf = capture(torch, lambda: [r.launch_unfused(handle) for r in runners], stream)
+    tails = {}
 
-    # warmup then exactly K timed steps (full graph rounds + eager remainder)
-    rounds_w = max(1, args.warmup // L)
-    time_graph(torch, g_all, rounds_w, stream)
-    full, rem = divmod(args.steps, L)
+    def replay_steps(n):
+        full, rem = divmod(n, L)
+        for _ in range(full):
+            g_all.replay()
+        if rem:
+            if rem not in tails:
+                raise RuntimeError("tail graph not captured")
+            tails[rem].replay()
+
+    for n in (args.steps, args.warmup):
+        if n % L and n % L not in tails:
+            tails[n % L] = capture(torch, lambda m=n % L: [r.launch(handle) for r in runners[:m]], stream)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        replay_steps(args.warmup)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
     with torch.cuda.stream(stream):  # replays and events on the same stream
         start.record(stream)
-        for _ in range(full):
-            g_all.replay()
-        for r in runners[:rem]:
-            r.launch(handle)
+        replay_steps(args.steps)
         end.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - wall0) * 1e3
     total_ms = start.elapsed_time(end)
-    log(f"timed {args.steps} steps: events {total_ms:.3f} ms, wall {wall_ms:.3f} ms")
+    log(f"timed {args.steps} steps ({args.steps // L} replays of a {L}-step graph + a {args.steps % L}-step graph): "
+        f"events {total_ms:.3f} ms, wall {wall_ms:.3f} ms")
     ms_per_step = total_ms / args.steps
     us_per_token = ms_per_step * 1000.0
 
@@ -606,16 +688,18 @@ def main() -> int:
         "unit": "us/token",
         "n_gpus": 1,
         "steps": args.steps,
-        "warmup": rounds_w * L,
+        "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "decode MoE layer, 1 token, hidden 2048, 512 routed experts top-10 + 1 shared, "
-                               "inter 512, affine Q4 g32 bf16 metadata, 48 distinct layers in an HBM slot pool "
-                               "(random slot permutation), HIP graph of 48 layer steps",
+        "config": {"workload": f"decode MoE layer, 1 token, hidden 2048, 512 routed experts top-10 + 1 shared, "
+                               f"inter 512, affine Q4 g32 bf16 metadata, {L} distinct layers in an HBM slot pool "
+                               f"(random slot permutation); step i runs layer i mod {L}; the {args.steps} timed steps "
+                               f"are {args.steps // L} replays of a {L}-step HIP graph plus one {args.steps % L}-step "
+                               f"graph",
                    "tokens": 1, "layers_rotated": L, "expert_bytes_per_token": expert_bytes,
                    "router_bytes_per_token": router_bytes},
         "hbm_gbps": round(layer_gbps, 1),

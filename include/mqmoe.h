@@ -28,16 +28,16 @@ extern "C" {
 #define MQ_ERR_DEVICE (-2)      /* no usable gfx950 device */
 #define MQ_ERR_LAUNCH (-3)      /* a HIP call or kernel launch failed */
 #define MQ_ERR_UNSUPPORTED (-4) /* valid request this build does not implement */
-#define MQ_ERR_TIMEOUT (-5)     /* a bounded in-kernel wait expired */
-#define MQ_ERR_NOMEM (-6)       /* library workspace allocation failed */
 
 #define MQ_F32 0
 #define MQ_BF16 1
 
 #define MQ_SLOT_BIT 0x80000000u /* route word: bit 31 set = pool slot */
 
-/* Bounds of the decode executor (models/flashnext/metal_runtime.py:26-31). */
-#define MQ_MAX_TOKENS 8
+/* Bounds of the decode entry points.  The reference executor takes at most 8
+ * tokens (models/flashnext/metal_runtime.py:26-31); mq_moe_decode and
+ * mq_moe_layer accept up to 64 (speculative-verify batches). */
+#define MQ_MAX_TOKENS 64
 #define MQ_MAX_EXPERTS 512
 #define MQ_MAX_TOP_K 10
 #define MQ_MAX_WIDTH 16384
@@ -98,7 +98,8 @@ typedef struct MqMoeArgs {
   void *out;              /* [tokens, hidden] T (combined) */
   void *gate_out;         /* optional [tokens, slots, inter] T (return_all diagnostics) */
   void *up_out;           /* optional [tokens, slots, inter] T */
-  void *act_out;          /* optional [tokens, slots(+1 with shared expert), inter] T */
+  void *act_out;          /* REQUIRED [tokens, slots(+1 with shared expert), inter] T: the
+                             SwiGLU activations (the library allocates nothing) */
   void *down_out;         /* optional [tokens, slots, hidden] T, per-slot down (return_all) */
   uint32_t tokens;
   uint32_t slots;
@@ -122,7 +123,7 @@ typedef struct MqRouteArgs {
   const uint16_t *logits_in;/* [tokens, experts] bf16 precomputed logits, or NULL */
   const uint16_t *shared_gate_w; /* [hidden] bf16 shared-expert gate row, or NULL */
   const uint32_t *slot_table;    /* [experts] pool slot per expert, or NULL (routes = expert ids) */
-  uint16_t *logits_out;     /* optional [tokens, experts] bf16 */
+  uint16_t *logits_out;     /* [tokens, experts] bf16, required unless logits_in is given */
   uint32_t *inds;           /* [tokens, top_k] expert ids, score-descending, ties by index */
   void *scores;             /* [tokens, top_k] renormalised scores */
   int score_dtype;          /* MQ_BF16 (bf16 arithmetic result) or MQ_F32 (widened) */
@@ -169,10 +170,9 @@ typedef struct MqGroupedArgs {
 /* 1 when a gfx950 device is usable from this process, else 0. */
 int mq_available(void);
 
-/* Allocate the library's per-device workspace (error flags, counters) on the
- * current device.  Entry points call it lazily, but a first call inside HIP
- * graph capture cannot allocate: call mq_init() (once per device) before
- * capturing.  Idempotent. */
+/* Resolve the library's per-device state (the device error flags, a static
+ * __device__ array; nothing is allocated) on the current device.  Entry
+ * points do this lazily; calling it first is optional.  Idempotent. */
 int mq_init(void);
 
 /* Copy the calling thread's last error message into buf (NUL-terminated). */
@@ -225,6 +225,33 @@ int mq_gather_qmv(const void *x, int x_dtype, int slot_input, const MqProjection
                   const uint32_t *routes, void *out, uint32_t tokens, uint32_t slots,
                   uint32_t in_features, uint32_t out_features, uint32_t expert_count,
                   uint32_t group_size, void *stream);
+
+/* ---- elementwise activations ---- */
+
+/* out = swiglu(gate, up) over n T values: MLX's swiglu as the reference's
+ * unfused up path calls it (models/flashnext/metal_runtime.py:895-907), with
+ * the fused Up epilogue's rounding points (:278-287): m = |g|, e = T(exp(m)),
+ * d = T(1 + e), s = T(1 / d), sig = g < 0 ? s : T(1 - s), out = T(T(g * sig) * u),
+ * exp correctly rounded to float32.  bf16 runs take the grouped kernels'
+ * four-at-a-time sequence, or with MQ_SWIGLU_SCALAR the decode kernels'
+ * per-element sequence (bit-identical by construction; both are exported so
+ * either can be checked on its own).  n < 2^31. */
+#define MQ_SWIGLU_SCALAR 1u
+int mq_swiglu(const void *gate, const void *up, void *out, uint64_t n, int dtype, uint32_t flags,
+              void *stream);
+
+/* out = sigmoid(x) over n T values with the same T-rounded sequence
+ * (mx.sigmoid of the shared-expert gate, models/flashnext/adaptive_topk.py:264). */
+int mq_sigmoid(const void *x, void *out, uint64_t n, int dtype, void *stream);
+
+/* Device check of the bf16 rounding the kernels use, over the float32 bit
+ * patterns [first, first + count) within [0, 2^32): adds to counts[0] the
+ * patterns where the kernels' round-to-bf16 differs from integer
+ * round-to-nearest-even with a canonical quiet NaN, and to counts[1] the
+ * non-NaN patterns where the one-instruction conversion differs from it.
+ * `counts` is a device array of two uint64 the caller zeroes.  No reference
+ * counterpart: it exists so the exactness claim is tested on each device. */
+int mq_bf16_round_check(uint64_t first, uint64_t count, unsigned long long *counts, void *stream);
 
 /* ---- router ---- */
 int mq_route_topk(const MqRouteArgs *args, void *stream);

@@ -36,7 +36,15 @@ int check_launch(const char *what) {
   return MQ_OK;
 }
 
+namespace {
+// Device error flags: one copy per device, zero-initialised when the code
+// object is loaded.  Host code reaches it only through the address that
+// hipGetSymbolAddress returns for the current device.
+__device__ __align__(256) unsigned int g_device_flags[kFlagWords];
+}  // namespace
+
 int workspace(DeviceWorkspace **out, hipStream_t stream) {
+  (void)stream;
   static std::mutex mu;
   static DeviceWorkspace per_device[64];
   static bool ready[64] = {};
@@ -45,19 +53,9 @@ int workspace(DeviceWorkspace **out, hipStream_t stream) {
   if (device < 0 || device >= 64) return fail(MQ_ERR_DEVICE, "device ordinal %d out of range", device);
   std::lock_guard<std::mutex> lock(mu);
   if (!ready[device]) {
-    // Allocating would invalidate a graph being captured on `stream`.
-    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
-    if (stream != nullptr && hipStreamIsCapturing(stream, &status) == hipSuccess &&
-        status != hipStreamCaptureStatusNone)
-      return fail(MQ_ERR_INVALID, "libmqmoe is not initialised on device %d: call mq_init() before graph capture",
-                  device);
-    DeviceWorkspace ws{};
-    MQ_TRY_HIP(hipMalloc(&ws.counters, kCounterSlots * sizeof(unsigned int)));
-    MQ_TRY_HIP(hipMalloc(&ws.flags, kCounterSlots * sizeof(unsigned int)));
-    MQ_TRY_HIP(hipMemset(ws.counters, 0, kCounterSlots * sizeof(unsigned int)));
-    MQ_TRY_HIP(hipMemset(ws.flags, 0, kCounterSlots * sizeof(unsigned int)));
-    MQ_TRY_HIP(hipDeviceSynchronize());
-    per_device[device] = ws;
+    void *flags = nullptr;
+    MQ_TRY_HIP(hipGetSymbolAddress(&flags, HIP_SYMBOL(g_device_flags)));
+    per_device[device].flags = static_cast<unsigned int *>(flags);
     ready[device] = true;
   }
   *out = &per_device[device];
@@ -89,7 +87,10 @@ extern "C" int mq_check_device_errors(void *stream, uint32_t *flags_out) {
   MQ_TRY_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
   unsigned int flags = 0;
   MQ_TRY_HIP(hipMemcpy(&flags, ws->flags, sizeof(flags), hipMemcpyDeviceToHost));
-  if (flags) MQ_TRY_HIP(hipMemset(ws->flags, 0, sizeof(unsigned int)));
+  if (flags) {
+    const unsigned int zero = 0u;
+    MQ_TRY_HIP(hipMemcpy(ws->flags, &zero, sizeof(zero), hipMemcpyHostToDevice));
+  }
   if (flags_out) *flags_out = flags;
   if (flags & MQ_DEVFLAG_BAD_ROUTE)
     return fail(MQ_ERR_INVALID, "a kernel skipped a route word that addressed no valid record or expert");

@@ -227,35 +227,6 @@ __device__ __forceinline__ float row_partial(const RowLoad<CPL> &r, const XLane<
   return acc;
 }
 
-// ------------------------------------------------------------------ SwiGLU
-// MLX's sigmoid sequence with each step rounded to T
-// (models/flashnext/metal_runtime.py:278-284): m=|g|; e=T(exp(m));
-// d=T(1+e); s=T(1/d); sig = g<0 ? s : T(1-s).  exp is the float32
-// exponential correctly rounded (evaluated in double).
-template <class TT>
-__device__ __forceinline__ float sigmoid_t(float g) {
-  if constexpr (TT::dtype == MQ_BF16) {
-    return sigmoid_bf16(g);  // the bf16 sequence (guarded float32 exp), shared with the grouped path
-  } else {
-    const float e = static_cast<float>(exp(static_cast<double>(fabsf(g))));
-    const float d = TT::round(__fadd_rn(1.0f, e));
-    const float s = TT::round(__fdiv_rn(1.0f, d));
-    const float om = TT::round(__fsub_rn(1.0f, s));
-    return g < 0.0f ? s : om;
-  }
-}
-
-// act = T(T(g * sigmoid_T(g)) * u) for T-valued g and u.
-template <class TT>
-__device__ __forceinline__ float swiglu_t(float g, float u) {
-  if constexpr (TT::dtype == MQ_BF16) {
-    return swiglu_bf16(g, u);
-  } else {
-    const float silu = TT::round(__fmul_rn(g, sigmoid_t<TT>(g)));
-    return TT::round(__fmul_rn(silu, u));
-  }
-}
-
 // ------------------------------------------------------------------ kernels
 
 // The shared expert's three projections, passed by value as a kernel argument.
@@ -473,14 +444,17 @@ enum SharedMode : int { kSharedNone = 0, kSharedY = 1, kSharedParts = 2, kShared
 // The T-rounded projections d go to LDS and wave 0 combines them in slot
 // order: acc += float(d) * float(score[t,s]) in float32 with no contraction
 // (models/flashnext/metal_runtime.py:291-336), then T(acc) and the shared
-// epilogue.  Padded slots (s >= keep) carry score 0 and are skipped.
+// epilogue.  With `generic` (group 64) every product is rounded to T first,
+// the order of the reference's weighted_combine in the score dtype
+// (metal_runtime.py:908-929).  Padded slots (s >= keep) carry score 0 and are
+// skipped.
 template <class TT, int SW, int CPL, int SPW, int R>
 __global__ __launch_bounds__(kThreads) void down_combine_kernel(
     const typename TT::storage *__restrict__ act, MqProjection down, SharedExpert shared,
     const uint32_t *__restrict__ routes, const void *__restrict__ scores, int score_dtype,
     const int32_t *__restrict__ keeps, int shared_mode, const typename TT::storage *__restrict__ shared_vec,
     const uint16_t *__restrict__ shared_gate, typename TT::storage *__restrict__ out, uint32_t tokens,
-    uint32_t slots, uint32_t hidden, uint32_t inter, uint32_t group, uint32_t dense_count,
+    uint32_t slots, uint32_t hidden, uint32_t inter, uint32_t group, uint32_t dense_count, bool generic,
     unsigned int *__restrict__ err) {
   using Sl = Slice<SW>;
   constexpr uint32_t kMaxSources = kMaxSlots + 1;
@@ -578,10 +552,16 @@ __global__ __launch_bounds__(kThreads) void down_combine_kernel(
   for (uint32_t s = 0; s < kMaxSlots; ++s) score[s] = readlane_f(score_lane, min(s, kMaxSlots - 1u));
   if (!fin_ok) return;
 
+  // Fused order: float32 products summed unrounded.  Generic order (group
+  // 64): every product rounded to T before the float32 slot-order sum.
   float acc = 0.0f;
 #pragma unroll
-  for (uint32_t s = 0; s < kMaxSlots; ++s)
-    if (s < keep) acc = __fadd_rn(acc, __fmul_rn(dsum[s + first_routed][ulane0], score[s]));
+  for (uint32_t s = 0; s < kMaxSlots; ++s) {
+    if (s < keep) {
+      const float prod = __fmul_rn(dsum[s + first_routed][ulane0], score[s]);
+      acc = __fadd_rn(acc, generic ? TT::round(prod) : prod);
+    }
+  }
   const float routed = TT::round(acc);
   float final_value = routed;
   if (shared_mode == kSharedY) {
@@ -753,7 +733,7 @@ void launch_down_r(const MqMoeArgs &a, const SharedExpert &shared, int shared_mo
   hipLaunchKernelGGL((down_combine_kernel<TT, SW, CPL, SPW, R>), grid, dim3(kThreads), 0, stream, act, a.down, shared,
                      a.routes, a.scores, a.score_dtype, keeps, shared_mode, shared_vec, a.shared_gate,
                      static_cast<S *>(a.out), a.tokens, a.slots, a.hidden, a.inter, a.group_size, a.expert_count,
-                     err);
+                     a.group_size == 64, err);
 }
 
 template <class TT, int SW, int CPL, int SPW, int R>
@@ -871,30 +851,9 @@ int moe_decode_t(const MqMoeArgs &a, hipStream_t stream, const MqRouteArgs *rout
   int rc = device_flags(&err, stream);
   if (rc) return rc;
 
-  // Activations: caller buffer or a grow-only library scratch buffer.
+  // Activations [pairs, inter] in the caller's act_out (checked by validate_moe_args).
   S *act = static_cast<S *>(a.act_out);
-  static thread_local void *scratch = nullptr;
-  static thread_local size_t scratch_bytes = 0;
-  static thread_local int scratch_dev = -1;
-  int device = 0;
-  MQ_TRY_HIP(hipGetDevice(&device));
-  const size_t need = static_cast<size_t>(pairs) * a.inter * sizeof(S);
-  if (act == nullptr) {
-    if (scratch == nullptr || scratch_bytes < need || scratch_dev != device) {
-      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-      if (stream != nullptr && hipStreamIsCapturing(stream, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
-        return fail(MQ_ERR_INVALID, "pass act_out when decoding inside graph capture");
-      if (scratch != nullptr && scratch_dev == device) {
-        MQ_TRY_HIP(hipDeviceSynchronize());
-        (void)hipFree(scratch);
-      }
-      scratch = nullptr;
-      MQ_TRY_HIP(hipMalloc(&scratch, need));
-      scratch_bytes = need;
-      scratch_dev = device;
-    }
-    act = static_cast<S *>(scratch);
-  }
+  (void)pairs;
 
   SharedExpert shared{};
   if (has_shared_expert)
@@ -974,8 +933,11 @@ int moe_decode_t(const MqMoeArgs &a, hipStream_t stream, const MqRouteArgs *rout
 int validate_moe_args(const MqMoeArgs &a, bool routed_layer) {
   if (a.x == nullptr) return fail(MQ_ERR_INVALID, "x is required");
   if (!routed_layer && a.routes == nullptr) return fail(MQ_ERR_INVALID, "x and routes are required");
-  if (a.tokens == 0 || a.tokens > 64) return fail(MQ_ERR_INVALID, "tokens must be in 1..64 (got %u)", a.tokens);
+  if (a.tokens == 0 || a.tokens > MQ_MAX_TOKENS)
+    return fail(MQ_ERR_INVALID, "tokens must be in 1..%d (got %u)", MQ_MAX_TOKENS, a.tokens);
   if (a.slots == 0 || a.slots > kMaxSlots) return fail(MQ_ERR_INVALID, "slots must be in 1..16 (got %u)", a.slots);
+  if (a.act_out == nullptr)
+    return fail(MQ_ERR_INVALID, "act_out is required ([tokens, slots (+1 with a shared expert), inter] activations)");
   int rc;
   if ((rc = validate_proj(&a.gate, "gate")) || (rc = validate_proj(&a.up, "up")) || (rc = validate_proj(&a.down, "down")))
     return rc;
@@ -986,6 +948,10 @@ int validate_moe_args(const MqMoeArgs &a, bool routed_layer) {
     if (!routed_layer && a.scores == nullptr) return fail(MQ_ERR_INVALID, "scores are required unless return_all is set");
     if (a.out == nullptr) return fail(MQ_ERR_INVALID, "out is required");
     if (a.score_dtype != MQ_F32 && a.score_dtype != MQ_BF16) return fail(MQ_ERR_INVALID, "bad score dtype");
+    if (a.group_size == 64 && a.x_dtype == MQ_BF16 && a.score_dtype == MQ_F32)
+      return fail(MQ_ERR_UNSUPPORTED,
+                  "group 64 combines in the score dtype, so bf16 activations with float32 scores give a float32 "
+                  "result: use MQ_DECODE_RETURN_ALL and combine on the caller's side");
     const int modes = (a.shared_y != nullptr) + (a.shared != nullptr) + (a.shared_expert != nullptr);
     if (modes > 1) return fail(MQ_ERR_INVALID, "provide shared_y, shared parts or a shared expert, not several");
     if ((a.shared != nullptr || a.shared_expert != nullptr) && a.shared_gate == nullptr)

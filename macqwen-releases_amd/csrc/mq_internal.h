@@ -18,15 +18,16 @@ int check_launch(const char *what);
     if (_e != hipSuccess) return ::mq::hip_fail(_e, #expr); \
   } while (0)
 
-// Per-device library workspace (counters, error flags).  Allocated once per
-// device on first use and zeroed; kernels restore every counter they use.
+// Per-device library state: the device error flags raised by kernels.  The
+// flags live in a file-scope __device__ array (one copy per device, loaded
+// with the code object), so the library never allocates device memory; the
+// per-device address is resolved once with hipGetSymbolAddress.
 struct DeviceWorkspace {
-  unsigned int *counters;  // kCounterSlots arrival counters
-  unsigned int *flags;     // error flags set by bounded waits
+  unsigned int *flags;  // kFlagWords words; word 0 holds the MQ_DEVFLAG_* bits
 };
-constexpr int kCounterSlots = 64;
-// The current device's workspace; allocates it on first use unless `stream`
-// is capturing a graph (then the call fails and asks for mq_init()).
+constexpr int kFlagWords = 64;
+// The current device's workspace (resolved on first use; no allocation, so
+// it is also safe inside graph capture).
 int workspace(DeviceWorkspace **out, hipStream_t stream);
 
 // ---------------------------------------------------------------- bf16

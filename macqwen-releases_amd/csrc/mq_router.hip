@@ -214,32 +214,12 @@ extern "C" int mq_route_topk(const MqRouteArgs *args, void *stream) {
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
 
-  // Logits go to the caller's buffer or a grow-only library scratch buffer.
+  // Logits go to the caller's buffer (the library allocates nothing).
   uint16_t *logits = a.logits_out;
-  static thread_local uint16_t *scratch = nullptr;
-  static thread_local size_t scratch_elems = 0;
-  static thread_local int scratch_dev = -1;
-  int device = 0;
-  MQ_TRY_HIP(hipGetDevice(&device));
   const bool need_logits = a.logits_in == nullptr;
   const bool need_shared = a.shared_gate != nullptr;
-  const size_t elems = static_cast<size_t>(a.tokens) * a.experts;
-  if (need_logits && logits == nullptr) {
-    if (scratch == nullptr || scratch_elems < elems || scratch_dev != device) {
-      hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-      if (s != nullptr && hipStreamIsCapturing(s, &cap) == hipSuccess && cap != hipStreamCaptureStatusNone)
-        return fail(MQ_ERR_INVALID, "pass logits_out when routing inside graph capture");
-      if (scratch != nullptr && scratch_dev == device) {
-        MQ_TRY_HIP(hipDeviceSynchronize());
-        (void)hipFree(scratch);
-      }
-      scratch = nullptr;
-      MQ_TRY_HIP(hipMalloc(&scratch, elems * sizeof(uint16_t)));
-      scratch_elems = elems;
-      scratch_dev = device;
-    }
-    logits = scratch;
-  }
+  if (need_logits && logits == nullptr)
+    return fail(MQ_ERR_INVALID, "logits_out is required when the logits are computed (logits_in is NULL)");
   // The shared-gate logit is parked in the shared_gate output, which the
   // select kernel then overwrites with its sigmoid.
   uint16_t *shared_logit = need_shared ? a.shared_gate : nullptr;

@@ -58,18 +58,33 @@ __device__ __forceinline__ float exp_bf16(float m) {
   return round_bf16_hw(e);
 }
 
+// bf16(1 / d) for a bf16 value d >= 2 (or inf), equal to the bf16 rounding of
+// the correctly rounded float32 quotient.  It takes the hardware reciprocal
+// (within 1 float32 ulp) instead of a division.  Normal results (d <= 2^126):
+// d = D * 2^k with D < 256; unless D is a power of two (then 1/d is exact
+// either way), the odd part D' >= 3 of D puts 1/d at a relative distance
+// >= 2^-8 / D' > 2^-16 from every bf16 rounding midpoint (an odd multiple of
+// 2^-9 times a power of two), far beyond the reciprocal's 2^-23, so both
+// round to the same bf16.  Denormal results (d > 2^126): v_rcp_f32 flushes
+// them to zero, so the reciprocal of d/4 (normal, exact scaling) is taken and
+// multiplied by 1/4, which rounds once onto the float32 denormal grid
+// (spacing 2^-149).  The bf16 denormal midpoints are odd multiples of 2^-134,
+// and 1/d = 2^-k / D' (D' odd >= 3) lies at least 2^-134 / 255 > 2^-142 from
+// each of them, while the two roundings move it by at most 2^-150 + 2^-150;
+// the correctly rounded float32 quotient is within 2^-150 as well, so both
+// give the same bf16.  d = inf gives 0 either way.
+__device__ __forceinline__ float recip_bf16(float d) {
+  const bool tiny = d > 0x1p126f;
+  const float r = __builtin_amdgcn_rcpf(tiny ? __fmul_rn(d, 0.25f) : d);
+  return round_bf16_hw(tiny ? __fmul_rn(r, 0.25f) : r);
+}
+
 // MLX bf16 sigmoid sequence (each step rounded to bf16, float32 exp correctly rounded).
-// bf16(1 / d) takes the hardware reciprocal (within 1 float32 ulp) instead of a
-// correctly rounded division: d is a bf16 value >= 2, so d = D * 2^k with D < 256;
-// unless D is a power of two (then 1/d is exact either way), the odd part D' >= 3
-// of D puts 1/d at a relative distance >= 2^-8 / D' > 2^-16 from every bf16
-// rounding midpoint (an odd multiple of 2^-9 times a power of two), far beyond
-// 2^-23, so both round to the same bf16.  d = inf gives 0 either way.
 __device__ __forceinline__ float sigmoid_bf16(float g) {
   const float m = fabsf(g);
   const float e = exp_bf16(m);
   const float d = round_bf16_hw(__fadd_rn(1.0f, e));
-  const float s = round_bf16_hw(__builtin_amdgcn_rcpf(d));
+  const float s = recip_bf16(d);
   const float om = round_bf16_hw(__fsub_rn(1.0f, s));
   return g < 0.0f ? s : om;
 }
@@ -104,10 +119,38 @@ __device__ __forceinline__ void swiglu_bf16_n(const float (&g)[N], const float (
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const float d = round_bf16_hw(__fadd_rn(1.0f, e[i]));
-    const float s = round_bf16_hw(__builtin_amdgcn_rcpf(d));
+    const float s = recip_bf16(d);
     const float om = round_bf16_hw(__fsub_rn(1.0f, s));
     const float silu = round_bf16_hw(__fmul_rn(g[i], g[i] < 0.0f ? s : om));
     out[i] = round_bf16(__fmul_rn(silu, u[i]));
+  }
+}
+
+// MLX's sigmoid sequence with each step rounded to T
+// (models/flashnext/metal_runtime.py:278-284): m=|g|; e=T(exp(m));
+// d=T(1+e); s=T(1/d); sig = g<0 ? s : T(1-s).  exp is the float32
+// exponential correctly rounded.
+template <class TT>
+__device__ __forceinline__ float sigmoid_t(float g) {
+  if constexpr (TT::dtype == MQ_BF16) {
+    return sigmoid_bf16(g);
+  } else {
+    const float e = static_cast<float>(exp(static_cast<double>(fabsf(g))));
+    const float d = TT::round(__fadd_rn(1.0f, e));
+    const float s = TT::round(__fdiv_rn(1.0f, d));
+    const float om = TT::round(__fsub_rn(1.0f, s));
+    return g < 0.0f ? s : om;
+  }
+}
+
+// act = T(T(g * sigmoid_T(g)) * u) for T-valued g and u.
+template <class TT>
+__device__ __forceinline__ float swiglu_t(float g, float u) {
+  if constexpr (TT::dtype == MQ_BF16) {
+    return swiglu_bf16(g, u);
+  } else {
+    const float silu = TT::round(__fmul_rn(g, sigmoid_t<TT>(g)));
+    return TT::round(__fmul_rn(silu, u));
   }
 }
 

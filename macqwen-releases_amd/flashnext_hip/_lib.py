@@ -18,19 +18,19 @@ MQ_ERR_INVALID = -1
 MQ_ERR_DEVICE = -2
 MQ_ERR_LAUNCH = -3
 MQ_ERR_UNSUPPORTED = -4
-MQ_ERR_TIMEOUT = -5
-MQ_ERR_NOMEM = -6
 MQ_F32 = 0
 MQ_BF16 = 1
 MQ_SLOT_BIT = 0x80000000
 MQ_DECODE_RETURN_ALL = 1
 MQ_DECODE_UNFUSED_UP = 2
+MQ_SWIGLU_SCALAR = 1
 
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTS = (
     "mq_available", "mq_init", "mq_last_error", "mq_check_device_errors", "mq_version",
     "mq_abi_struct_size", "mq_record_layout",
     "mq_q4_unpack", "mq_q4_dequant", "mq_q4_qmv", "mq_gather_qmv",
+    "mq_swiglu", "mq_sigmoid", "mq_bf16_round_check",
     "mq_route_topk", "mq_moe_decode", "mq_moe_layer", "mq_grouped_workspace_size",
     "mq_moe_grouped", "mq_pool_refill_async",
 )
@@ -163,6 +163,9 @@ def _declare(lib) -> None:
         "mq_q4_dequant": ([vp, vp, vp, vp, u32, u32, u32, vp], i32),
         "mq_q4_qmv": ([vp, i32, vp, vp, vp, vp, u32, u32, u32, u32, vp], i32),
         "mq_gather_qmv": ([vp, i32, i32, c.POINTER(MqProjection), vp, vp, u32, u32, u32, u32, u32, u32, vp], i32),
+        "mq_swiglu": ([vp, vp, vp, u64, i32, u32, vp], i32),
+        "mq_sigmoid": ([vp, vp, u64, i32, vp], i32),
+        "mq_bf16_round_check": ([u64, u64, vp, vp], i32),
         "mq_route_topk": ([c.POINTER(MqRouteArgs), vp], i32),
         "mq_moe_decode": ([c.POINTER(MqMoeArgs), vp], i32),
         "mq_moe_layer": ([c.POINTER(MqRouteArgs), c.POINTER(MqMoeArgs), vp], i32),
@@ -204,8 +207,8 @@ def load(path: str | os.PathLike | None = None):
 
 
 def init_device() -> None:
-    """Allocate the library workspace on the current device (before any graph
-    capture); a no-op when no gfx950 device is visible."""
+    """Resolve the library's per-device state (its device error flags) on the
+    current device; a no-op when no gfx950 device is visible."""
     lib = _LIB
     if lib is not None and lib.mq_available() == 1:
         check(lib.mq_init(), lib)

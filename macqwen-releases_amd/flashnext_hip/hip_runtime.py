@@ -37,7 +37,8 @@ BITS = 4
 
 @dataclass(frozen=True)
 class Q4G32Projection:
-    """Packed expert rows consumed by one gate, up, or down projection."""
+    """One projection's expert bank: uint32 nibble words ``[E, out, in/8]`` and
+    bf16 group scales and biases ``[E, out, in/group]``."""
 
     weight: Any
     scales: Any
@@ -46,7 +47,8 @@ class Q4G32Projection:
 
 @dataclass(frozen=True)
 class HipCapabilities:
-    """Backend probe result exposed as attributes and mapping-like keys."""
+    """What the probe found (library, device, injected backend); readable as
+    attributes or by key, like the reference's capability mapping."""
 
     available: bool
     supports_custom_moe: bool
@@ -337,8 +339,17 @@ class HipMoEExecutor:
         args.group_size = self.group_size
         keep_alive = [route_words]
 
-        g64_generic = scores is not None and not return_all and self.group_size == 64
-        if return_all or scores is None or g64_generic:
+        # Group 64 with bf16 activations and float32 scores combines in float32
+        # (the reference's weighted_combine promotes to the score dtype,
+        # metal_runtime.py:908-929) and returns float32: per-slot outputs from
+        # the kernels, the combine here.  Every other scored call combines in
+        # the down kernel, which follows the group-64 order itself.
+        g64_f32 = (scores is not None and not return_all and self.group_size == 64 and x.dtype == torch.bfloat16
+                   and getattr(scores, "dtype", None) not in (torch.bfloat16,))
+        if g64_f32 and shared_expert is not None:
+            raise ValueError("shared_expert with group 64, bf16 x and float32 scores is not supported: "
+                             "pass shared_y or shared and shared_gate")
+        if return_all or scores is None or g64_f32:
             gate_out = torch.empty((tokens, slots, inter), dtype=x.dtype, device=dev)
             up_out = torch.empty_like(gate_out)
             act = torch.empty_like(gate_out)
@@ -352,9 +363,7 @@ class HipMoEExecutor:
                 return gate_out, up_out, down_out
             if scores is None:
                 return down_out
-            # Group-64 keeps the reference's generic reduction in the score
-            # dtype (metal_runtime.py:914-929).
-            out = weighted_combine(down_out, route_words, scores.to(dev))
+            out = weighted_combine(down_out, route_words, scores.to(dev).float())
             if shared_y is not None:
                 out = out + shared_y.to(dev).reshape(out.shape)
             elif shared is not None:

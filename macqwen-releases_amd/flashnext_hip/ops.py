@@ -81,6 +81,35 @@ def quantized_matmul(x, w, scales, biases, transpose: bool = True, group_size: i
     return y
 
 
+def swiglu(gate, up, *, scalar: bool = False) -> torch.Tensor:
+    """MLX ``swiglu(gate, up)`` with the fused Up epilogue's rounding points
+    (``models/flashnext/metal_runtime.py:278-287, 895-907``): every step rounded
+    to the input dtype.  ``scalar`` selects the per-element device sequence of
+    the decode kernels instead of the four-at-a-time one of the grouped kernels
+    (bit-identical)."""
+    g = require_cuda(gate, "gate")
+    u = require_cuda(up, "up")
+    dt = act_dtype(g, "gate")
+    if u.dtype != g.dtype or u.shape != g.shape:
+        raise ValueError("gate and up must have the same shape and dtype")
+    out = torch.empty_like(g)
+    lib = _lib.load()
+    _lib.check(lib.mq_swiglu(ptr(g), ptr(u), ptr(out), g.numel(), dt,
+                             _lib.MQ_SWIGLU_SCALAR if scalar else 0, stream_handle()), lib)
+    return out
+
+
+def sigmoid(x) -> torch.Tensor:
+    """``mx.sigmoid`` with every step of the sequence rounded to x's dtype
+    (the shared-expert gate, ``models/flashnext/adaptive_topk.py:264``)."""
+    x = require_cuda(x, "x")
+    dt = act_dtype(x)
+    out = torch.empty_like(x)
+    lib = _lib.load()
+    _lib.check(lib.mq_sigmoid(ptr(x), ptr(out), x.numel(), dt, stream_handle()), lib)
+    return out
+
+
 def dense_projection(weight, scales, biases) -> "_lib.MqProjection":
     """MqProjection over dense expert arrays ``[E, out, in/8]``."""
     p = _lib.MqProjection()

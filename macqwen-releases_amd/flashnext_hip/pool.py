@@ -77,36 +77,51 @@ class HipExpertPool:
         if self.slots < MIN_SLOTS:
             raise ValueError("expert pool is too small for one decode layer")
         self.buffer = torch.zeros(HEADER_SIZE + self.slots * self.stride, dtype=torch.uint8, device=device)
-        self._slot_of: "OrderedDict[tuple, int]" = OrderedDict()
-        self._free = list(range(self.slots - 1, -1, -1))
+        # (layer, expert) -> slot, least recently used first.
+        self._lru: "OrderedDict[tuple, int]" = OrderedDict()
+        self._unused = 0  # slots [_unused, slots) have never held a record
         self.hits = 0
         self.misses = 0
         self._lib = _lib.load()
 
+    def _claim_slot(self) -> int:
+        """A never-used slot (lowest first) while any is left, else the slot of
+        the least recently used key, which is dropped."""
+        if self._unused < self.slots:
+            self._unused += 1
+            return self._unused - 1
+        _key, slot = self._lru.popitem(last=False)
+        return slot
+
     # ------------------------------------------------------------ LRU (expert_pool.py:88-110)
     def assign(self, layer: int, experts):
-        """Return ``({expert: slot}, [(expert, slot) to fill])`` for one layer."""
-        slot_of = self._slot_of
-        slots, misses = {}, []
-        for expert in experts:
+        """Slots for one layer's experts: ``({expert: slot}, [(expert, slot), ...])``.
+
+        The order rules are the reference pool's, which its tests fix: every
+        requested expert already resident is refreshed first, in request order,
+        so none of them can be evicted by this call's misses while older keys
+        remain; the misses then claim slots in request order (untouched slots
+        from slot 0 upwards, then the least recently used keys).  The second
+        list names the slots whose records must be filled.
+        """
+        requested = list(experts)
+        placed: dict = {}
+        for expert in requested:
             key = (layer, expert)
-            slot = slot_of.get(key)
+            slot = self._lru.pop(key, None)
             if slot is not None:
-                slot_of.move_to_end(key)
-                slots[expert] = slot
-        self.hits += len(slots)
-        for expert in experts:
-            if expert in slots:
-                continue
-            if self._free:
-                slot = self._free.pop()
-            else:
-                _old, slot = slot_of.popitem(last=False)
-            slot_of[(layer, expert)] = slot
-            slots[expert] = slot
-            misses.append((expert, slot))
-        self.misses += len(misses)
-        return slots, misses
+                self._lru[key] = slot  # re-inserted at the most recent end
+                placed[expert] = slot
+        self.hits += len(placed)
+        to_fill = []
+        for expert in requested:
+            if expert not in placed:
+                slot = self._claim_slot()
+                self._lru[(layer, expert)] = slot
+                placed[expert] = slot
+                to_fill.append((expert, slot))
+        self.misses += len(to_fill)
+        return placed, to_fill
 
     # ------------------------------------------------------------ refill (expert_pool.py:112-145)
     def fill(self, layer: int, misses, store: HostRecordStore, *, compute_stream=None, copy_stream=None):

@@ -59,7 +59,7 @@ def route(x: torch.Tensor, gate_w: torch.Tensor | None, top_k: int, *, threshold
     routes = torch.empty((tokens, top_k), dtype=torch.int32, device=dev)
     keeps = torch.empty((tokens,), dtype=torch.int32, device=dev)
     logits_out = None
-    if logits is None and keep_logits:
+    if logits is None:  # the library allocates nothing: the logits need a buffer either way
         logits_out = torch.empty((tokens, experts), dtype=torch.bfloat16, device=dev)
     shared_gate = None
     if shared_gate_w is not None:
@@ -82,4 +82,4 @@ def route(x: torch.Tensor, gate_w: torch.Tensor | None, top_k: int, *, threshold
     a.threshold, a.min_keep, a.blend = float(threshold), int(min_keep), float(blend)
     lib = _lib.load()
     _lib.check(lib.mq_route_topk(a, stream_handle()), lib)
-    return RouteResult(inds, scores, raw, routes, keeps, logits_out, shared_gate)
+    return RouteResult(inds, scores, raw, routes, keeps, logits_out if keep_logits else None, shared_gate)

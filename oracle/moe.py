@@ -144,6 +144,27 @@ def down_combine(down_t, scores, dtype: str = "bf16", *, score_dtype: str = "f32
     return round_t(routed, dtype)
 
 
+def generic_decode_combine(down_bits, scores_bits, *, shared_y=None, keeps=None):
+    """Group-64 decode combine: the reference keeps ``weighted_combine`` in the
+    score dtype and adds ``shared_y`` afterwards (``metal_runtime.py:908-929``).
+    With bf16 scores every product is rounded to bf16, the kept slots are summed
+    in float32 in slot order and rounded once, then ``shared_y`` is added in
+    bf16.  Padded slots (score 0) add nothing and are skipped.
+    """
+    d = bf16_to_f32(down_bits)
+    s = bf16_to_f32(scores_bits)
+    tokens, slots, _hidden = d.shape
+    acc = np.zeros((tokens, d.shape[2]), dtype=np.float32)
+    for j in range(slots):
+        active = np.ones(tokens, dtype=bool) if keeps is None else (np.asarray(keeps) > j)
+        prod = bf16_to_f32(f32_to_bf16((d[:, j, :] * s[:, j][:, None]).astype(np.float32)))
+        acc = np.where(active[:, None], (acc + prod).astype(np.float32), acc)
+    total = bf16_to_f32(f32_to_bf16(acc))
+    if shared_y is None:
+        return f32_to_bf16(total)
+    return f32_to_bf16((total + bf16_to_f32(shared_y)).astype(np.float32))
+
+
 def generic_combine(y_bits, scores_bits, shared_gate_bits=None, shared_bits=None):
     """bf16 ``(y * scores[..., None]).sum(-2) + shared_gate * shared``.
 
@@ -201,8 +222,11 @@ def shared_gate_value(x_bits, w_sg_bits):
 def decode_layer(x, routes_experts, scores, records: ExpertRecordSet, *,
                  dtype: str = "bf16", score_dtype: str = "f32", keeps=None,
                  shared_y=None, shared=None, shared_gate=None,
-                 shared_gate_weight=None, return_all: bool = False):
+                 shared_gate_weight=None, return_all: bool = False, combine: str = "fused"):
     """Fused-executor decode semantics (``MetalMoEExecutor.execute`` with scores).
+
+    ``combine="generic"`` is the group-64 order (:func:`generic_decode_combine`,
+    bf16 scores and activations only).
 
     ``routes_experts``: expert ids ``[T, K]`` (slot indirection already
     resolved).  When ``records.shared`` and ``shared_gate_weight`` are given the
@@ -231,6 +255,12 @@ def decode_layer(x, routes_experts, scores, records: ExpertRecordSet, *,
         sg = shared_gate_value(x if dtype == "bf16" else f32_to_bf16(xf), shared_gate_weight)
         shared_y = f32_to_bf16(bf16_to_f32(sg)[:, None] * to_f32(sd, dtype)) if dtype == "bf16" else \
             (bf16_to_f32(sg)[:, None] * to_f32(sd, dtype)).astype(np.float32)
+    if combine == "generic":
+        if dtype != "bf16" or score_dtype != "bf16":
+            raise ValueError("the generic decode combine is defined here for bf16 activations and scores")
+        if shared is not None:
+            shared_y = f32_to_bf16(to_f32(shared, dtype) * to_f32(shared_gate, dtype).reshape(tokens, 1))
+        return generic_decode_combine(down_t, scores, shared_y=shared_y, keeps=keeps)
     return down_combine(down_t, scores, dtype, score_dtype=score_dtype, shared_y=shared_y,
                         shared=shared, shared_gate=shared_gate, keeps=keeps)
 

@@ -15,6 +15,11 @@ from oracle import bf16, q4
 # and cosine >= 0.9999; the reference's own tests use rtol 2e-2 / atol 3e-3).
 RTOL = 1e-2
 ATOL = 3e-3
+# The reference's own elementwise tolerance for bf16 executor outputs
+# (models/flashnext/tests/unit/test_metal_runtime.py:321-350), used where a
+# check covers millions of elements, whose tails rtol 1e-2 would make a test of
+# accumulated rounding ties rather than of the kernel.
+REF_RTOL = 2e-2
 MIN_COSINE = 0.9999
 MAX_REL = 1e-2
 

@@ -210,3 +210,96 @@ def test_many_token_shared_epilogues_equal_single_token_calls(torch_mod):
             one = ex.execute(x[t:t + 1], r[t:t + 1], dev, scores=sc[t:t + 1], **kw1)
             torch.cuda.synchronize()
             assert torch.equal(full[t:t + 1].view(torch.int16), one.view(torch.int16)), (sorted(kw), t)
+
+
+def _build_layer(torch, hidden, inter, group, seed):
+    from flashnext_hip.layout import make_layout
+    from flashnext_hip.moe_block import LayerWeights
+
+    records = make_records(E, hidden, inter, seed=seed, group=group)
+    shared = make_records(1, hidden, inter, seed=seed + 1, group=group)
+    slots = 24
+    perm = np.random.default_rng(seed + 2).permutation(slots)[:E].astype(np.int32)
+    img, _ = pool_from_banks(records, perm, slots, hidden, inter, group)
+    wg = bf16_normal((E, hidden), seed=seed + 3, std=0.02)
+    wsg = bf16_normal((1, hidden), seed=seed + 4, std=0.02)
+    sh = tuple(tuple(t[:1] for t in to_dev_bank(b)) for b in (shared.gate, shared.up, shared.down))
+    weights = LayerWeights(make_layout(hidden, inter, group), torch.from_numpy(img).cuda(),
+                           torch.from_numpy(perm).cuda(), to_dev_bf16(wg), to_dev_bf16(wsg).reshape(-1), sh)
+    recs = moe.ExpertRecordSet(records.gate, records.up, records.down, shared=(shared.gate, shared.up, shared.down))
+    return weights, recs, perm, wg, wsg
+
+
+@pytest.fixture(scope="module")
+def checkpoint_shape_layers(torch_mod):
+    say("building 2560/640 layers at group 32 and group 64")
+    return {group: _build_layer(torch_mod, 2560, 640, group, seed=560 + group) for group in (32, 64)}
+
+
+@pytest.mark.parametrize("group", [32, 64])
+@pytest.mark.parametrize("tokens", [3, 8, 9, 40])
+def test_moe_block_checkpoint_shape_adaptive_keep(torch_mod, checkpoint_shape_layers, group, tokens):
+    """``_moe_call`` at the checkpoint shape (hidden 2560, inter 640: the
+    non-fast 640-wide down path) with the chat default keep threshold 0.85
+    (``adaptive_topk.py:75-232``) on both paths: the routed layer up to 8
+    tokens (fused float32 combine at group 32, the generic bf16 order at group
+    64, ``metal_runtime.py:908-929``) and the grouped path beyond."""
+    torch = torch_mod
+    say(f"case: moe block 2560/640 g{group} tokens={tokens} threshold=0.85")
+    from flashnext_hip import _lib
+    from flashnext_hip.moe_block import MoEBlock
+
+    hidden = 2560
+    weights, recs, perm, wg, wsg = checkpoint_shape_layers[group]
+    block = MoEBlock(weights, K, threshold=0.85, min_keep=2)
+    x = bf16_normal((tokens, hidden), seed=570 + tokens + group)
+    out = block(to_dev_bf16(x))
+    torch.cuda.synchronize()
+    assert _lib.check_device_errors() == 0
+    ref = orouter.route(x, wg, K, threshold=0.85, min_keep=2, slot_table=perm.astype(np.uint32))
+    r = block.last_route
+    assert np.array_equal(r.routes.cpu().numpy().view(np.uint32), ref["routes"])
+    assert np.array_equal(from_dev_bf16(r.scores), ref["scores"])
+    assert np.array_equal(r.keeps.cpu().numpy(), ref["keeps"])
+    assert (ref["keeps"] < K).any(), "the threshold should drop slots for some token"
+    got = bf16.bf16_to_f32(from_dev_bf16(out))
+    if tokens <= 8:
+        assert block.last_path == "fused"
+        want = moe.decode_layer(x, ref["inds"], ref["scores"], recs, score_dtype="bf16", shared_gate_weight=wsg,
+                                keeps=ref["keeps"], combine="generic" if group == 64 else "fused")
+        assert_close(got, bf16.bf16_to_f32(want), f"fused block g{group} T={tokens}")
+        return
+    assert block.last_path == "grouped"
+    width = ref["width"]
+    tiles, _ = moe.prefill_layer(x, ref["inds"][:, :width], ref["scores"][:, :width], recs,
+                                 shared_gate_weight=wsg, weights="bf16")
+    assert_close(got, bf16.bf16_to_f32(tiles), f"grouped block g{group} T={tokens} (bf16 tiles)")
+
+
+def test_group64_executor_shared_expert_generic_order(torch_mod, checkpoint_shape_layers):
+    """The group-64 executor with an in-kernel shared expert: the routed slots
+    combine in the generic bf16 order and the shared expert is added (it is
+    not dropped), against the oracle."""
+    torch = torch_mod
+    say("case: group-64 executor with shared expert")
+    from flashnext_hip.hip_runtime import HipMoEExecutor
+    from flashnext_hip import router
+
+    hidden, inter, tokens = 2560, 640, 3
+    weights, recs, perm, wg, wsg = checkpoint_shape_layers[64]
+    banks = {n: to_dev_bank(b) for n, b in (("gate_proj", recs.gate), ("up_proj", recs.up),
+                                             ("down_proj", recs.down))}
+    sh = {n: tuple(t[:1] for t in to_dev_bank(b)) for n, b in zip(("gate_proj", "up_proj", "down_proj"), recs.shared)}
+    x = bf16_normal((tokens, hidden), seed=580)
+    ref = orouter.route(x, wg, K)
+    sg = router.route(to_dev_bf16(x), to_dev_bf16(wg), K, shared_gate_w=to_dev_bf16(wsg)).shared_gate
+    ex = HipMoEExecutor(E, hidden, K, group_size=64)
+    out = ex.execute(to_dev_bf16(x), torch.from_numpy(ref["inds"].astype(np.int64)).cuda(), banks,
+                     scores=to_dev_bf16(ref["scores"]), shared_gate=sg, shared_expert=sh)
+    torch.cuda.synchronize()
+    want = moe.decode_layer(x, ref["inds"], ref["scores"], recs, score_dtype="bf16", shared_gate_weight=wsg,
+                            combine="generic")
+    assert_close(bf16.bf16_to_f32(from_dev_bf16(out)), bf16.bf16_to_f32(want), "g64 executor + shared expert")
+    no_shared = ex.execute(to_dev_bf16(x), torch.from_numpy(ref["inds"].astype(np.int64)).cuda(), banks,
+                           scores=to_dev_bf16(ref["scores"]))
+    assert not torch.equal(out.view(torch.int16), no_shared.view(torch.int16))

@@ -240,6 +240,81 @@ def test_generic_combine_bf16_order():
     assert bf16.bf16_to_f32(moe.generic_combine(y, s)).tolist() == [[1.25, 2.0]]
 
 
+def test_generic_decode_combine_rounds_each_product():
+    # Group 64 keeps weighted_combine in the score dtype (metal_runtime.py:908-929):
+    # 1.5078125 * 1.5078125 = 2.27349853515625 rounds up to 2.28125 in bf16, so
+    # three such products sum to 6.84375 (0x40DB); the fused float32 order sums
+    # the unrounded products to 6.82049560546875, which rounds to 6.8125 (0x40DA).
+    d = np.full((1, 3, 1), 0x3FC1, dtype=np.uint16)
+    s = np.full((1, 3), 0x3FC1, dtype=np.uint16)
+    assert moe.generic_decode_combine(d, s).tolist() == [[0x40DB]]
+    assert moe.down_combine(d, s, score_dtype="bf16").tolist() == [[0x40DA]]
+    one = np.array([[0x3F80]], dtype=np.uint16)
+    assert moe.generic_decode_combine(d, s, shared_y=one).tolist() == [[0x40FB]]  # 7.84375
+    assert moe.generic_decode_combine(d, s, keeps=[1]).tolist() == [[0x4012]]     # 2.28125
+
+
+def _bf16_exact(value):
+    """Nearest-even bf16 of a rational (8 significant bits, denormals below 2^-126)."""
+    from fractions import Fraction
+
+    v = Fraction(value)
+    if v == 0:
+        return Fraction(0)
+    sign = -1 if v < 0 else 1
+    a = abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    quantum = Fraction(2) ** (max(e, -126) - 7)
+    q, r = divmod(a, quantum)
+    if r * 2 > quantum or (r * 2 == quantum and q % 2 == 1):
+        q += 1
+    return sign * q * quantum
+
+
+def _f32_exact(value):
+    """Nearest-even float32 of a rational (24 significant bits, denormals below 2^-126)."""
+    from fractions import Fraction
+
+    v = Fraction(value)
+    if v == 0:
+        return Fraction(0)
+    sign = -1 if v < 0 else 1
+    a = abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    quantum = Fraction(2) ** (max(e, -126) - 23)
+    q, r = divmod(a, quantum)
+    if r * 2 > quantum or (r * 2 == quantum and q % 2 == 1):
+        q += 1
+    return sign * q * quantum
+
+
+def test_swiglu_denormal_tail_matches_exact_rationals():
+    # For gates near -88 the sigmoid 1/(1+e^88) lies below 2^-126: the bf16
+    # sequence keeps it as a denormal (a flushing reciprocal would give -0).
+    # Every step is recomputed here with exact rationals and float64 exp.
+    import math
+    from fractions import Fraction
+
+    gates = np.arange(0xC2A0, 0xC2B2, dtype=np.uint16)  # -80.0 .. -89.0
+    up = np.full(gates.shape, 0x3F80, dtype=np.uint16)
+    got = moe.swiglu(gates, up)
+    for g_bits, out_bits in zip(gates.tolist(), got.tolist()):
+        g = Fraction(float(bf16.bf16_to_f32(np.uint16(g_bits))))
+        m = -g
+        e = _bf16_exact(_f32_exact(Fraction(math.exp(float(m)))))
+        d = _bf16_exact(1 + e)
+        sig = _bf16_exact(_f32_exact(1 / d))
+        act = _bf16_exact(_f32_exact(_bf16_exact(_f32_exact(g * sig)) * 1))
+        want = float(act)
+        assert float(bf16.bf16_to_f32(np.uint16(out_bits))) == want, (hex(g_bits), hex(out_bits), want)
+    tail = dict(zip(gates.tolist(), got.tolist()))
+    assert (tail[0xC2AF], tail[0xC2B0], tail[0xC2B1]) == (0x8395, 0x8336, 0x82DD)  # -87.5, -88.0, -88.5
+
+
 # ---------------------------------------------------------------- pool / layout
 def test_layout_reference_constants():
     kat = KATS["layout_checkpoint_g32"]
