@@ -278,6 +278,21 @@ uint64_t mq_grouped_workspace_size(uint32_t tokens, uint32_t slots, uint32_t hid
                                    uint32_t inter, uint32_t route_keys, int shared);
 int mq_moe_grouped(const MqGroupedArgs *args, void *stream);
 
+/* mq_moe_grouped with the library's own static scratch instead of a
+ * workspace: it calls no allocator (no hipMalloc, hipFree or allocating
+ * runtime routine), for callers that cannot allocate -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation.  No
+ * counterpart in the reference.  args->workspace and workspace_bytes are
+ * ignored.  The scratch is a file-scope __device__ array of
+ * MQ_GROUPED_STATIC_SCRATCH_BYTES per device (held until the process ends);
+ * a call whose mq_grouped_workspace_size() exceeds it fails with
+ * MQ_ERR_INVALID before anything is launched.  Every call on one device shares
+ * that device's scratch: calls that overlap on one device (different streams
+ * or threads without ordering) race.  64 MiB covers the 4096-token prefill
+ * chunk at hidden 2048 / inter 512 over 512 experts with a shared expert. */
+#define MQ_GROUPED_STATIC_SCRATCH_BYTES (64ull << 20)
+int mq_moe_grouped_static(const MqGroupedArgs *args, void *stream);
+
 /* ---- expert slot pool refill (models/flashnext/expert_pool.py:112-145) ----
  * Copy n records of record_bytes each from pinned host memory to pool slots
  * (slot i lands at pool + pool_header + slots[i] * pool_stride) on

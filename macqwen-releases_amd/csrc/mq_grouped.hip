@@ -27,6 +27,8 @@
 // Weights are dequantized as bf16(fma(q, s, b)) (one float32 rounding, then
 // bf16); every output row is computed independently of its position in a
 // tile, so the result does not depend on the order rows land in a tile.
+#include <mutex>
+
 #include "mq_internal.h"
 #include "mq_select.h"
 
@@ -962,9 +964,11 @@ extern "C" uint64_t mq_grouped_workspace_size(uint32_t tokens, uint32_t slots, u
   return make_layout(tokens, slots, hidden, inter, route_keys, shared != 0).total;
 }
 
-extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
-  if (args == nullptr) return fail(MQ_ERR_INVALID, "args is NULL");
-  const MqGroupedArgs &a = *args;
+namespace mq {
+namespace {
+
+// Argument checks shared by both entry points; fills the key space and layout.
+int grouped_validate(const MqGroupedArgs &a, KeySpace *ks_out, Layout *l_out) {
   if (a.x == nullptr || a.routes == nullptr || a.y == nullptr)
     return fail(MQ_ERR_INVALID, "x, routes and y are required");
   if (a.tokens == 0 || a.slots == 0 || a.slots > 64) return fail(MQ_ERR_INVALID, "tokens must be positive and slots 1..64");
@@ -987,17 +991,27 @@ extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
   if (a.out != nullptr && a.scores == nullptr) return fail(MQ_ERR_INVALID, "scores are required to combine into out");
   const KeySpace ks = key_space(a);
   const Layout l = make_layout(a.tokens, a.slots, a.hidden, a.inter, ks.slots + ks.ids, shared_expert);
-  if (a.workspace == nullptr || a.workspace_bytes < l.total)
-    return fail(MQ_ERR_INVALID, "workspace needs %llu bytes (got %llu)", static_cast<unsigned long long>(l.total),
-                static_cast<unsigned long long>(a.workspace_bytes));
   if (static_cast<uint64_t>(a.tokens) * a.hidden * 2u >= (1ull << 31) ||
       static_cast<uint64_t>(l.rows) * a.inter * 2u >= (1ull << 31))
     return fail(MQ_ERR_UNSUPPORTED, "activation buffers must stay below 2 GiB");
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  *ks_out = ks;
+  *l_out = l;
+  return MQ_OK;
+}
+
+// The whole grouped call with its scratch at `ws` (at least the layout's bytes).
+int grouped_call(const MqGroupedArgs &a, uint8_t *ws, uint64_t ws_bytes, hipStream_t s) {
+  KeySpace ks;
+  Layout l;
+  int rc = grouped_validate(a, &ks, &l);
+  if (rc) return rc;
+  if (ws == nullptr || ws_bytes < l.total)
+    return fail(MQ_ERR_INVALID, "workspace needs %llu bytes (got %llu)", static_cast<unsigned long long>(l.total),
+                static_cast<unsigned long long>(ws_bytes));
+  const bool shared_expert = a.shared_expert != nullptr;
   unsigned int *err = nullptr;
   if ((rc = device_flags_grouped(&err, s))) return rc;
 
-  uint8_t *ws = static_cast<uint8_t *>(a.workspace);
   uint32_t *counts = reinterpret_cast<uint32_t *>(ws + l.counts);
   uint32_t *cursor = reinterpret_cast<uint32_t *>(ws + l.cursor);
   uint32_t *row_key = reinterpret_cast<uint32_t *>(ws + l.row_key);
@@ -1093,4 +1107,54 @@ extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
     if ((rc = check_launch("grouped_combine_kernel"))) return rc;
   }
   return MQ_OK;
+}
+
+// Scratch of mq_moe_grouped_static: one copy per device, held until the
+// process ends.  Host code never uses the array's name as an address: the
+// device address of the current device's copy is resolved once per device
+// with hipGetSymbolAddress and kept in g_static_scratch.
+constexpr uint64_t kStaticScratchBytes = MQ_GROUPED_STATIC_SCRATCH_BYTES;
+__device__ __align__(256) uint8_t scratch[kStaticScratchBytes];
+
+int static_scratch(uint8_t **out) {
+  static std::mutex mu;
+  static uint8_t *per_device[64];
+  int device = 0;
+  MQ_TRY_HIP(hipGetDevice(&device));
+  if (device < 0 || device >= 64) return fail(MQ_ERR_DEVICE, "device ordinal %d out of range", device);
+  std::lock_guard<std::mutex> lock(mu);
+  if (per_device[device] == nullptr) {
+    void *ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    per_device[device] = static_cast<uint8_t *>(ptr);
+  }
+  *out = per_device[device];
+  return MQ_OK;
+}
+
+}  // namespace
+}  // namespace mq
+
+extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
+  if (args == nullptr) return fail(MQ_ERR_INVALID, "args is NULL");
+  return grouped_call(*args, static_cast<uint8_t *>(args->workspace), args->workspace_bytes,
+                      static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mq_moe_grouped_static(const MqGroupedArgs *args, void *stream) {
+  if (args == nullptr) return fail(MQ_ERR_INVALID, "args is NULL");
+  const MqGroupedArgs &a = *args;
+  KeySpace ks;
+  Layout l;
+  int rc = grouped_validate(a, &ks, &l);
+  if (rc) return rc;
+  if (l.total > kStaticScratchBytes)
+    return fail(MQ_ERR_INVALID,
+                "mq_moe_grouped_static: this call needs %llu bytes of scratch, above the static maximum of %llu "
+                "(MQ_GROUPED_STATIC_SCRATCH_BYTES); use mq_moe_grouped with a workspace",
+                static_cast<unsigned long long>(l.total), static_cast<unsigned long long>(kStaticScratchBytes));
+  uint8_t *scratch_ptr = nullptr;
+  if ((rc = static_scratch(&scratch_ptr))) return rc;
+  return grouped_call(a, scratch_ptr, kStaticScratchBytes, static_cast<hipStream_t>(stream));
 }

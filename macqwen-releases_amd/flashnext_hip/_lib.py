@@ -32,7 +32,7 @@ EXPORTS = (
     "mq_q4_unpack", "mq_q4_dequant", "mq_q4_qmv", "mq_gather_qmv",
     "mq_swiglu", "mq_sigmoid", "mq_bf16_round_check",
     "mq_route_topk", "mq_moe_decode", "mq_moe_layer", "mq_grouped_workspace_size",
-    "mq_moe_grouped", "mq_pool_refill_async",
+    "mq_moe_grouped", "mq_moe_grouped_static", "mq_pool_refill_async",
 )
 
 
@@ -171,6 +171,7 @@ def _declare(lib) -> None:
         "mq_moe_layer": ([c.POINTER(MqRouteArgs), c.POINTER(MqMoeArgs), vp], i32),
         "mq_grouped_workspace_size": ([u32, u32, u32, u32, u32, i32], u64),
         "mq_moe_grouped": ([c.POINTER(MqGroupedArgs), vp], i32),
+        "mq_moe_grouped_static": ([c.POINTER(MqGroupedArgs), vp], i32),
         "mq_pool_refill_async": ([vp, u64, u64, u32, vp, vp, u32, u64, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
