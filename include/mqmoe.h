@@ -183,13 +183,14 @@ int mq_last_error(char *buf, uint32_t max_len);
  * else MQ_ERR_INVALID with the flags described by mq_last_error(). */
 int mq_check_device_errors(void *stream, uint32_t *flags_out);
 #define MQ_DEVFLAG_BAD_ROUTE 1u /* a route word addressed no valid record/expert */
+#define MQ_DEVFLAG_BAD_ROW 2u   /* an x row index (MqGatherArgs.x_rows) was >= x_count */
 
 /* Library version as major*10000 + minor*100 + patch. */
 int mq_version(void);
 
 /* sizeof() of the ABI structs as compiled into the library, so bindings can
  * verify their layout: which = 0 MqProjection, 1 MqMoeArgs, 2 MqRouteArgs,
- * 3 MqGroupedArgs; 0 for an unknown id. */
+ * 3 MqGroupedArgs, 4 MqGatherArgs; 0 for an unknown id. */
 uint64_t mq_abi_struct_size(int which);
 
 /* ---- record layout (models/flashnext/slab_pack.py:96-149) ---- */
@@ -277,6 +278,37 @@ int mq_moe_layer(const MqRouteArgs *route, const MqMoeArgs *moe, void *stream);
 uint64_t mq_grouped_workspace_size(uint32_t tokens, uint32_t slots, uint32_t hidden,
                                    uint32_t inter, uint32_t route_keys, int shared);
 int mq_moe_grouped(const MqGroupedArgs *args, void *stream);
+
+/* One grouped projection: out[r, :] = bf16(W_{route[r]} . x[x_rows[r]]) for
+ * r < rows, fp32 accumulate over bf16(s*q + b) weights.  This is
+ * mx.gather_qmm(x, w, scales, biases, rhs_indices, transpose=True,
+ * group_size, bits=4, sorted_indices) at the prefill / verify call shape
+ * (models/flashnext/expert_cache.py:799-810, called three times per pass from
+ * _issue at :1790-1806 on rows sorted by expert): the rows are counting-sorted
+ * by route key on the device and run through the same MFMA GEMM as
+ * mq_moe_grouped's down projection, with no combine.  Row order in `routes`
+ * does not change any value (sorted_indices is only a hint there too).
+ * Route words as in MqMoeArgs (plain ids < expert_count, or MQ_SLOT_BIT|slot
+ * with a pool projection); a word that addresses nothing raises
+ * MQ_DEVFLAG_BAD_ROUTE and its row reads zero weights; an x_rows entry
+ * >= x_count raises MQ_DEVFLAG_BAD_ROW and its row reads zero inputs. */
+typedef struct MqGatherArgs {
+  const uint16_t *x;        /* [x_count, in_width] bf16 */
+  const uint32_t *x_rows;   /* [rows] x row of each output row, or NULL: row r reads x row r
+                               (then x_count >= rows) */
+  const uint32_t *routes;   /* [rows] route words */
+  uint16_t *out;            /* [rows, out_width] bf16 */
+  MqProjection w;
+  void *workspace;          /* device scratch of mq_gather_qmm_workspace_size() bytes */
+  uint64_t workspace_bytes;
+  uint32_t x_count, rows, in_width, out_width;
+  uint32_t expert_count;    /* dense experts addressed by plain route ids (0 with a pool) */
+  uint32_t group_size;
+} MqGatherArgs;
+
+/* Workspace bytes for mq_gather_qmm; `route_keys` as for mq_grouped_workspace_size. */
+uint64_t mq_gather_qmm_workspace_size(uint32_t rows, uint32_t route_keys);
+int mq_gather_qmm(const MqGatherArgs *args, void *stream);
 
 /* mq_moe_grouped with the library's own static scratch instead of a
  * workspace: it calls no allocator (no hipMalloc, hipFree or allocating

@@ -94,6 +94,8 @@ extern "C" int mq_check_device_errors(void *stream, uint32_t *flags_out) {
   if (flags_out) *flags_out = flags;
   if (flags & MQ_DEVFLAG_BAD_ROUTE)
     return fail(MQ_ERR_INVALID, "a kernel skipped a route word that addressed no valid record or expert");
+  if (flags & MQ_DEVFLAG_BAD_ROW)
+    return fail(MQ_ERR_INVALID, "a gather row index was at or past the end of x");
   if (flags) return fail(MQ_ERR_INVALID, "device error flags 0x%x", flags);
   return MQ_OK;
 }
@@ -104,6 +106,7 @@ extern "C" uint64_t mq_abi_struct_size(int which) {
     case 1: return sizeof(MqMoeArgs);
     case 2: return sizeof(MqRouteArgs);
     case 3: return sizeof(MqGroupedArgs);
+    case 4: return sizeof(MqGatherArgs);
     default: return 0;
   }
 }

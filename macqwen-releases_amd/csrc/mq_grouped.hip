@@ -48,6 +48,14 @@ constexpr uint32_t kSharedWord = 0xfffffffeu;  // tile word of the shared expert
 constexpr uint32_t kDeadWord = 0xffffffffu;    // tile word of rows with invalid route words
 constexpr int kPlanThreads = 1024;
 
+// GEMM modes: gate/up (two projections of the token rows, SwiGLU epilogue),
+// down (one projection of the sorted act rows, output scattered to y) and
+// gather (one projection of caller rows picked through a row map, output
+// scattered back to the caller's row order).
+constexpr int kModeGateUp = 0;
+constexpr int kModeDown = 1;
+constexpr int kModeGather = 2;
+
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2_t2 __attribute__((ext_vector_type(2)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
@@ -107,6 +115,28 @@ Layout make_layout(uint32_t tokens, uint32_t slots, uint32_t hidden, uint32_t in
   l.n_tiles = off;  off = align256(off + 4);
   l.act = off;      off = align256(off + uint64_t(l.rows) * inter * 2);
   l.y_shared = off; off = align256(off + (shared ? uint64_t(tokens) * hidden * 2 : 0));
+  l.total = off;
+  return l;
+}
+
+// Workspace of the gather entry point: the sort arrays and the row map.
+struct GatherLayout {
+  uint64_t counts, cursor, row_key, order, tiles, n_tiles, xmap, total;
+  uint32_t max_tiles;
+};
+
+GatherLayout make_gather_layout(uint32_t rows, uint32_t route_keys) {
+  GatherLayout l{};
+  const uint64_t keys = uint64_t(route_keys) + 2u;
+  l.max_tiles = static_cast<uint32_t>((rows + kTileRows - 1) / kTileRows + std::min<uint64_t>(rows, keys));
+  uint64_t off = 0;
+  l.counts = off;   off = align256(off + keys * 4);
+  l.cursor = off;   off = align256(off + keys * 4);
+  l.row_key = off;  off = align256(off + uint64_t(rows) * 4);
+  l.order = off;    off = align256(off + uint64_t(rows) * 4);
+  l.tiles = off;    off = align256(off + uint64_t(l.max_tiles) * sizeof(GroupTile));
+  l.n_tiles = off;  off = align256(off + 4);
+  l.xmap = off;     off = align256(off + uint64_t(rows) * 4);
   l.total = off;
   return l;
 }
@@ -348,6 +378,19 @@ __global__ __launch_bounds__(kSortThreads) void grouped_scatter_lds_kernel(const
   }
 }
 
+// Gather row map: xmap[i] = x row of sorted row i (~0u, with a flag, when the
+// caller's row index is past the end of x).
+__global__ void gather_map_kernel(const uint32_t *__restrict__ order, const uint32_t *__restrict__ x_rows,
+                                  uint32_t rows, uint32_t x_count, uint32_t *__restrict__ xmap,
+                                  unsigned int *__restrict__ err) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows) return;
+  const uint32_t r = x_rows[order[i]];
+  const bool bad = r >= x_count;
+  xmap[i] = bad ? ~0u : r;
+  if (bad) raise_flag(err, MQ_DEVFLAG_BAD_ROW);
+}
+
 // ------------------------------------------------------------------ GEMM
 template <int B>
 __device__ __forceinline__ float ubyte_to_f32(uint32_t v) {
@@ -550,8 +593,11 @@ struct XcdItems {
 };
 
 struct GemmParams {
-  const uint16_t *x;     // gate/up: token activations [tokens, K]; down: act [rows, K] in sorted order
+  const uint16_t *x;     // gate/up: token activations [tokens, K]; down: act [rows, K] in sorted order;
+                         // gather: the caller's rows [x_count, K]
   uint32_t x_bytes;
+  const uint32_t *xmap;  // gather: x row of each sorted row (~0u: none)
+  uint32_t xmap_bytes;
   MqProjection w0, w1;   // gate/up: gate, up; down: down (w1 unused)
   MqProjection s0, s1;   // the shared expert's matching projections (dense, expert 0) or unused
   const GroupTile *tiles;
@@ -559,7 +605,7 @@ struct GemmParams {
   const uint32_t *n_tiles;
   const uint32_t *order;
   uint32_t order_bytes;
-  uint16_t *out;         // gate/up: act [rows, N] sorted; down: y [routed_rows, N]
+  uint16_t *out;         // gate/up: act [rows, N] sorted; down: y [routed_rows, N]; gather: [rows, N]
   uint16_t *out_shared;  // down: the shared expert's output [tokens, N] or null
   uint32_t slots, routed_rows, K, N, dense_count;
   unsigned int *err;
@@ -571,8 +617,8 @@ struct GemmParams {
 struct Item {
   uint32_t j;       // index in the XCD's item list (uniform)
   uint4 tile;       // GroupTile: word, start, count (all zero past the end)
-  uint32_t xraw;    // gate/up: `order` entry of this thread's tile row
-  uint32_t dst[4];  // down: `order` entries of this lane's tile rows in the four slabs
+  uint32_t xraw;    // gate/up: `order` entry of this thread's tile row; gather: its x row
+  uint32_t dst[4];  // down, gather: `order` entries of this lane's tile rows in the four slabs
 };
 
 __device__ __forceinline__ void fetch_tile(Item &m, uint32_t j, const XcdItems &it, __amdgpu_buffer_rsrc_t tr) {
@@ -580,35 +626,38 @@ __device__ __forceinline__ void fetch_tile(Item &m, uint32_t j, const XcdItems &
   m.tile = buf_load16(tr, j < it.count ? it.tile(j) * 16u : kOutOfRange);
 }
 
-// Second fetch step, once the tile record has arrived: the sorted-row entries.
-template <bool DOWN>
-__device__ __forceinline__ void fetch_rows(Item &m, __amdgpu_buffer_rsrc_t orr, int tid) {
+// Second fetch step, once the tile record has arrived: the sorted-row entries
+// (`orr`: order, `xmr`: the gather row map).
+template <int MODE>
+__device__ __forceinline__ void fetch_rows(Item &m, __amdgpu_buffer_rsrc_t orr, __amdgpu_buffer_rsrc_t xmr, int tid) {
   const uint32_t start = m.tile.y, count = m.tile.z;
-  if constexpr (DOWN) {
+  if constexpr (MODE != kModeGateUp) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const uint32_t i = 32u * t + (static_cast<uint32_t>(tid) & 31u);
       m.dst[t] = buf_load4(orr, i < count ? (start + i) * 4u : kOutOfRange);
     }
-  } else {
+  }
+  if constexpr (MODE != kModeDown) {
     const uint32_t i = static_cast<uint32_t>(tid) / kXParts;
-    m.xraw = buf_load4(orr, i < count ? (start + i) * 4u : kOutOfRange);
+    m.xraw = buf_load4(MODE == kModeGather ? xmr : orr, i < count ? (start + i) * 4u : kOutOfRange);
   }
 }
 
 // This thread's activation row for the item's X loads (~0u: none).
-template <bool DOWN>
+template <int MODE>
 __device__ __forceinline__ uint32_t x_source(const Item &m, const GemmParams &p, int tid) {
   const uint32_t i = static_cast<uint32_t>(tid) / kXParts;
   if (i >= m.tile.z) return ~0u;
-  if constexpr (DOWN) return m.tile.y + i;
+  if constexpr (MODE == kModeDown) return m.tile.y + i;
+  else if constexpr (MODE == kModeGather) return m.xraw;
   else return m.xraw < p.routed_rows ? m.xraw / p.slots : m.xraw - p.routed_rows;
 }
 
 // The lane's weight row of an item.  Gate/up: waves 0-3 stream gate rows and
-// waves 4-7 the up rows of the same 128 features; down: wave w streams rows
-// 32 w .. +31 of the item's 256 output features.
-template <bool DOWN, int G>
+// waves 4-7 the up rows of the same 128 features; down and gather: wave w
+// streams rows 32 w .. +31 of the item's 256 output features.
+template <int MODE, int G>
 __device__ __forceinline__ WRow weight_row(const Item &m, const GemmParams &p, const XcdItems &it,
                                            uint32_t nb_count, uint32_t wave, int lane) {
   const bool valid = m.j < it.count;
@@ -617,7 +666,7 @@ __device__ __forceinline__ WRow weight_row(const Item &m, const GemmParams &p, c
   const bool shared = word == kSharedWord;
   ExpertPtrs e;
   uint32_t row;
-  if constexpr (DOWN) {
+  if constexpr (MODE != kModeGateUp) {
     if (shared) e = expert_ptrs(p.s0, 0u, p.N, p.K, G, 1u);
     else e = expert_ptrs(p.w0, word, p.N, p.K, G, p.dense_count);
     row = nb * kDownFeatures + 32u * wave + (static_cast<uint32_t>(lane) & 31u);
@@ -707,8 +756,8 @@ __device__ __forceinline__ void gateup_epilogue(const f32x16_t (&acc)[4], uint16
   else gateup_epilogue_half<false>(acc, xb + fw * kExchange, m, p, nb, fw, lane, slab);
 }
 
-// Down epilogue: the bf16 outputs go back to y[token, slot] (or the shared
-// expert's row).
+// Down and gather epilogue: the bf16 outputs go back to the row's `order`
+// entry: y[token, slot] (or the shared expert's row), or the gather row.
 __device__ __forceinline__ void down_epilogue(const f32x16_t (&acc)[4], const Item &m, const GemmParams &p,
                                               uint32_t nb, uint32_t wave, int lane, const bool (&slab)[4]) {
   const uint32_t count = uniform(m.tile.z);
@@ -732,7 +781,7 @@ __device__ __forceinline__ void down_epilogue(const f32x16_t (&acc)[4], const It
 // Pipeline state carried across stages and items: the weight ring, the load
 // cursor (row and stage, NS stages ahead of compute), and the activation
 // registers of the next stage with their source rows.
-template <bool DOWN, int NS, int G>
+template <int MODE, int NS, int G>
 struct Pipe {
   WStage ring[NS];
   WRow lw;
@@ -757,14 +806,14 @@ struct Pipe {
         if (xrow < 32u * NSLAB) store_xstage(xb, xv, xrow, xpart);  // rows past the active slabs are never read
         __syncthreads();
         const bool last = u == NS - 1 && s + 1u == S;
-        if (last) xsrc_next = x_source<DOWN>(n, p, tid);
+        if (last) xsrc_next = x_source<MODE>(n, p, tid);
         load_xstage(xv, xr, last ? xsrc_next : xsrc, p.K, last ? 0u : s + 1u, xpart);
         stage_mma<G, NSLAB>(acc, xb + xl_off, ring[u], lw, p.K, ls, half);
         if (++ls == S) {
           // The load cursor finished an item.  With NS == S it was already
           // in the next item n, and this is compute's last stage of c.
           ls = 0;
-          lw = weight_row<DOWN, G>(last ? n2 : n, p, it, nb_count, wave, lane);
+          lw = weight_row<MODE, G>(last ? n2 : n, p, it, nb_count, wave, lane);
         }
       }
     }
@@ -780,10 +829,10 @@ struct Pipe {
 // the next item start while the current one finishes (NS <= stages per item,
 // so the load cursor is at most one item ahead), and tile records and sorted
 // rows are fetched two items ahead.
-template <bool DOWN, int NS, int G>
+template <int MODE, int NS, int G>
 __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmParams p) {
   __shared__ __align__(16) uint16_t xs[2 * kXTile];
-  constexpr uint32_t kFeat = DOWN ? kDownFeatures : kGateUpFeatures;
+  constexpr uint32_t kFeat = MODE == kModeGateUp ? kGateUpFeatures : kDownFeatures;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const uint32_t wave = wave_id();
@@ -796,27 +845,28 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmParam
   const __amdgpu_buffer_rsrc_t tr = make_rsrc(p.tiles, p.tiles_bytes);
   const __amdgpu_buffer_rsrc_t orr = make_rsrc(p.order, p.order_bytes);
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x, p.x_bytes);
+  const __amdgpu_buffer_rsrc_t xmr = make_rsrc(p.xmap, MODE == kModeGather ? p.xmap_bytes : 0u);
 
   Item c, n, n2;  // the compute item and the next two
   fetch_tile(c, it.first, it, tr);
   fetch_tile(n, it.first + it.stride, it, tr);
   fetch_tile(n2, it.first + 2u * it.stride, it, tr);
-  fetch_rows<DOWN>(c, orr, tid);
-  fetch_rows<DOWN>(n, orr, tid);
+  fetch_rows<MODE>(c, orr, xmr, tid);
+  fetch_rows<MODE>(n, orr, xmr, tid);
 
   // Load cursor: NS stages ahead of the compute cursor.
-  Pipe<DOWN, NS, G> pp;
-  pp.lw = weight_row<DOWN, G>(c, p, it, nb_count, wave, lane);
+  Pipe<MODE, NS, G> pp;
+  pp.lw = weight_row<MODE, G>(c, p, it, nb_count, wave, lane);
   pp.ls = 0;
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
     load_wstage<G>(pp.ring[u], pp.lw, p.K, pp.ls, half);
     if (++pp.ls == S) {
       pp.ls = 0;
-      pp.lw = weight_row<DOWN, G>(n, p, it, nb_count, wave, lane);
+      pp.lw = weight_row<MODE, G>(n, p, it, nb_count, wave, lane);
     }
   }
-  pp.xsrc = x_source<DOWN>(c, p, tid);
+  pp.xsrc = x_source<MODE>(c, p, tid);
   pp.xsrc_next = ~0u;
   load_xstage(pp.xv, xr, pp.xsrc, p.K, 0u, xpart);
 
@@ -839,7 +889,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmParam
       default: pp.template run<4>(acc, xs, n, n2, p, it, nb_count, wave, lane, tid, S, xr); break;
     }
     // Every item starts on LDS tile 0; its last stage used tile (S - 1) & 1.
-    if constexpr (DOWN) down_epilogue(acc, c, p, nb, wave, lane, slab);
+    if constexpr (MODE != kModeGateUp) down_epilogue(acc, c, p, nb, wave, lane, slab);
     else gateup_epilogue(acc, xs + ((S - 1u) & 1u) * kXTile, c, p, nb, wave, lane, slab);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -848,7 +898,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmParam
     c = n;
     n = n2;
     fetch_tile(n2, c.j + 2u * it.stride, it, tr);
-    fetch_rows<DOWN>(n, orr, tid);
+    fetch_rows<MODE>(n, orr, xmr, tid);
     pp.xsrc = pp.xsrc_next;
     if (c.j >= it.count) break;  // uniform
     count = uniform(c.tile.z);
@@ -930,21 +980,23 @@ int validate_proj_grouped(const MqProjection &p, const char *name) {
 // compute cursor.  Two stages ahead keep the kernel within 256 registers per
 // lane with the B-fragment read-ahead (four stages spill; measured on the
 // 4096-token chunk: 4 stages 918-928 us, 2 stages 897-909 us per call).
-template <bool DOWN, int NS>
+template <int MODE, int NS>
 int launch_gemm_ns(const GemmParams &p, uint32_t group, uint32_t grid, hipStream_t s) {
   if (group == 32)
-    hipLaunchKernelGGL((grouped_gemm_kernel<DOWN, NS, 32>), dim3(grid), dim3(kGemmThreads), 0, s, p);
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NS, 32>), dim3(grid), dim3(kGemmThreads), 0, s, p);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<DOWN, NS, 64>), dim3(grid), dim3(kGemmThreads), 0, s, p);
-  return check_launch(DOWN ? "grouped_gemm_kernel (down)" : "grouped_gemm_kernel (gate/up)");
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NS, 64>), dim3(grid), dim3(kGemmThreads), 0, s, p);
+  return check_launch(MODE == kModeGateUp ? "grouped_gemm_kernel (gate/up)"
+                      : MODE == kModeDown ? "grouped_gemm_kernel (down)"
+                                          : "grouped_gemm_kernel (gather)");
 }
 
-template <bool DOWN>
+template <int MODE>
 int launch_gemm(const GemmParams &p, uint32_t group, uint32_t grid, hipStream_t s) {
   const uint32_t stages = p.K / kKS;
-  if (stages % 2 == 0) return launch_gemm_ns<DOWN, 2>(p, group, grid, s);
-  if (stages % 3 == 0) return launch_gemm_ns<DOWN, 3>(p, group, grid, s);
-  return launch_gemm_ns<DOWN, 1>(p, group, grid, s);
+  if (stages % 2 == 0) return launch_gemm_ns<MODE, 2>(p, group, grid, s);
+  if (stages % 3 == 0) return launch_gemm_ns<MODE, 3>(p, group, grid, s);
+  return launch_gemm_ns<MODE, 1>(p, group, grid, s);
 }
 
 KeySpace key_space(const MqGroupedArgs &a) {
@@ -999,6 +1051,63 @@ int grouped_validate(const MqGroupedArgs &a, KeySpace *ks_out, Layout *l_out) {
   return MQ_OK;
 }
 
+struct SortBufs {
+  uint32_t *counts, *cursor, *row_key, *order;
+  GroupTile *tiles;
+  uint32_t *n_tiles;
+};
+
+// Counting sort of `rows` rows by route key (rows past routed_rows belong to
+// the shared group): `order` lists the row indices grouped by key, `tiles`
+// the (word, start, count) tiles.  One block when the rows and keys fit,
+// else zero / count / plan / scatter.
+int sort_rows(const uint32_t *routes, uint32_t routed_rows, uint32_t rows, const KeySpace &ks, const SortBufs &b,
+              unsigned int *err, hipStream_t s) {
+  int rc;
+  if (ks.size() <= kSingleSortKeys && rows <= 16u * kPlanThreads) {
+    const uint32_t kpt = ceil_div(rows, kPlanThreads);
+    const uint32_t hist_bytes = ks.size() * 4u;
+    if (kpt <= 4)
+      hipLaunchKernelGGL(grouped_sort_single_kernel<4>, dim3(1), dim3(kPlanThreads), hist_bytes, s, routes,
+                         routed_rows, rows, ks, b.order, b.tiles, b.n_tiles, err);
+    else
+      hipLaunchKernelGGL(grouped_sort_single_kernel<16>, dim3(1), dim3(kPlanThreads), hist_bytes, s, routes,
+                         routed_rows, rows, ks, b.order, b.tiles, b.n_tiles, err);
+    return check_launch("grouped_sort_single_kernel");
+  }
+  hipLaunchKernelGGL(grouped_zero_kernel, dim3(ceil_div(ks.size(), 256)), dim3(256), 0, s, b.counts, ks.size());
+  if ((rc = check_launch("grouped_zero_kernel"))) return rc;
+  const bool lds_sort = ks.size() <= kLdsKeys;
+  const uint32_t hist_bytes = ks.size() * 4u;
+  if (lds_sort)
+    hipLaunchKernelGGL(grouped_count_lds_kernel, dim3(ceil_div(rows, kSortRows)), dim3(kSortThreads), hist_bytes, s,
+                       routes, routed_rows, rows, ks, b.counts, b.row_key, err);
+  else
+    hipLaunchKernelGGL(grouped_count_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, s, routes, routed_rows, rows,
+                       ks, b.counts, b.row_key, err);
+  if ((rc = check_launch("grouped_count_kernel"))) return rc;
+  hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, b.counts, b.cursor, b.tiles, b.n_tiles,
+                     ks);
+  if ((rc = check_launch("grouped_plan_kernel"))) return rc;
+  if (lds_sort)
+    hipLaunchKernelGGL(grouped_scatter_lds_kernel, dim3(ceil_div(rows, kSortRows)), dim3(kSortThreads), hist_bytes, s,
+                       b.row_key, rows, ks, b.cursor, b.order);
+  else
+    hipLaunchKernelGGL(grouped_scatter_kernel, dim3(ceil_div(rows, 256)), dim3(256), 0, s, b.row_key, rows, b.cursor,
+                       b.order);
+  return check_launch("grouped_scatter_kernel");
+}
+
+// GEMM grid bound: one 8-wave block per CU, a multiple of 8 (XCD-aware item
+// schedule).
+int gemm_blocks(uint32_t *resident) {
+  int device = 0, cus = 0;
+  MQ_TRY_HIP(hipGetDevice(&device));
+  MQ_TRY_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
+  *resident = std::max(8u, (static_cast<uint32_t>(cus > 0 ? cus : 256) / 8u) * 8u);
+  return MQ_OK;
+}
+
 // The whole grouped call with its scratch at `ws` (at least the layout's bytes).
 int grouped_call(const MqGroupedArgs &a, uint8_t *ws, uint64_t ws_bytes, hipStream_t s) {
   KeySpace ks;
@@ -1012,55 +1121,18 @@ int grouped_call(const MqGroupedArgs &a, uint8_t *ws, uint64_t ws_bytes, hipStre
   unsigned int *err = nullptr;
   if ((rc = device_flags_grouped(&err, s))) return rc;
 
-  uint32_t *counts = reinterpret_cast<uint32_t *>(ws + l.counts);
-  uint32_t *cursor = reinterpret_cast<uint32_t *>(ws + l.cursor);
-  uint32_t *row_key = reinterpret_cast<uint32_t *>(ws + l.row_key);
   uint32_t *order = reinterpret_cast<uint32_t *>(ws + l.order);
   GroupTile *tiles = reinterpret_cast<GroupTile *>(ws + l.tiles);
   uint32_t *n_tiles = reinterpret_cast<uint32_t *>(ws + l.n_tiles);
   uint16_t *act = reinterpret_cast<uint16_t *>(ws + l.act);
   uint16_t *y_shared = shared_expert ? reinterpret_cast<uint16_t *>(ws + l.y_shared) : nullptr;
   const uint32_t routed_rows = a.tokens * a.slots;
+  const SortBufs sb{reinterpret_cast<uint32_t *>(ws + l.counts), reinterpret_cast<uint32_t *>(ws + l.cursor),
+                    reinterpret_cast<uint32_t *>(ws + l.row_key), order, tiles, n_tiles};
+  if ((rc = sort_rows(a.routes, routed_rows, l.rows, ks, sb, err, s))) return rc;
 
-  if (ks.size() <= kSingleSortKeys && l.rows <= 16u * kPlanThreads) {
-    const uint32_t kpt = ceil_div(l.rows, kPlanThreads);
-    const uint32_t hist_bytes = ks.size() * 4u;
-    if (kpt <= 4)
-      hipLaunchKernelGGL(grouped_sort_single_kernel<4>, dim3(1), dim3(kPlanThreads), hist_bytes, s, a.routes,
-                         routed_rows, l.rows, ks, order, tiles, n_tiles, err);
-    else
-      hipLaunchKernelGGL(grouped_sort_single_kernel<16>, dim3(1), dim3(kPlanThreads), hist_bytes, s, a.routes,
-                         routed_rows, l.rows, ks, order, tiles, n_tiles, err);
-    if ((rc = check_launch("grouped_sort_single_kernel"))) return rc;
-  } else {
-    hipLaunchKernelGGL(grouped_zero_kernel, dim3(ceil_div(ks.size(), 256)), dim3(256), 0, s, counts, ks.size());
-    if ((rc = check_launch("grouped_zero_kernel"))) return rc;
-    const bool lds_sort = ks.size() <= kLdsKeys;
-    const uint32_t hist_bytes = ks.size() * 4u;
-    if (lds_sort)
-      hipLaunchKernelGGL(grouped_count_lds_kernel, dim3(ceil_div(l.rows, kSortRows)), dim3(kSortThreads), hist_bytes, s,
-                         a.routes, routed_rows, l.rows, ks, counts, row_key, err);
-    else
-      hipLaunchKernelGGL(grouped_count_kernel, dim3(ceil_div(l.rows, 256)), dim3(256), 0, s, a.routes, routed_rows,
-                         l.rows, ks, counts, row_key, err);
-    if ((rc = check_launch("grouped_count_kernel"))) return rc;
-    hipLaunchKernelGGL(grouped_plan_kernel, dim3(1), dim3(kPlanThreads), 0, s, counts, cursor, tiles, n_tiles, ks);
-    if ((rc = check_launch("grouped_plan_kernel"))) return rc;
-    if (lds_sort)
-      hipLaunchKernelGGL(grouped_scatter_lds_kernel, dim3(ceil_div(l.rows, kSortRows)), dim3(kSortThreads), hist_bytes,
-                         s, row_key, l.rows, ks, cursor, order);
-    else
-      hipLaunchKernelGGL(grouped_scatter_kernel, dim3(ceil_div(l.rows, 256)), dim3(256), 0, s, row_key, l.rows, cursor,
-                         order);
-    if ((rc = check_launch("grouped_scatter_kernel"))) return rc;
-  }
-
-  int device = 0, cus = 0;
-  MQ_TRY_HIP(hipGetDevice(&device));
-  MQ_TRY_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device));
-  // One 8-wave block per CU, a multiple of 8 (XCD-aware item schedule).
-  const uint32_t resident = std::max(8u, (static_cast<uint32_t>(cus > 0 ? cus : 256) / 8u) * 8u);
-
+  uint32_t resident = 0;
+  if ((rc = gemm_blocks(&resident))) return rc;
   GemmParams gp{};
   gp.x = a.x;
   gp.x_bytes = a.tokens * a.hidden * 2u;
@@ -1083,7 +1155,7 @@ int grouped_call(const MqGroupedArgs &a, uint8_t *ws, uint64_t ws_bytes, hipStre
   gp.dense_count = a.expert_count;
   gp.err = err;
   const uint32_t gu_items = l.max_tiles * ceil_div(a.inter, kGateUpFeatures);
-  if ((rc = launch_gemm<false>(gp, a.group_size, std::min(ceil_div(gu_items, 8) * 8u, resident), s))) return rc;
+  if ((rc = launch_gemm<kModeGateUp>(gp, a.group_size, std::min(ceil_div(gu_items, 8) * 8u, resident), s))) return rc;
 
   GemmParams dp = gp;
   dp.x = act;
@@ -1097,7 +1169,7 @@ int grouped_call(const MqGroupedArgs &a, uint8_t *ws, uint64_t ws_bytes, hipStre
   dp.K = a.inter;
   dp.N = a.hidden;
   const uint32_t dn_items = l.max_tiles * ceil_div(a.hidden, kDownFeatures);
-  if ((rc = launch_gemm<true>(dp, a.group_size, std::min(ceil_div(dn_items, 8) * 8u, resident), s))) return rc;
+  if ((rc = launch_gemm<kModeDown>(dp, a.group_size, std::min(ceil_div(dn_items, 8) * 8u, resident), s))) return rc;
 
   if (a.out != nullptr) {
     const uint16_t *shared_vec = shared_expert ? y_shared : a.shared;
@@ -1135,6 +1207,76 @@ int static_scratch(uint8_t **out) {
 
 }  // namespace
 }  // namespace mq
+
+extern "C" uint64_t mq_gather_qmm_workspace_size(uint32_t rows, uint32_t route_keys) {
+  return make_gather_layout(rows, route_keys).total;
+}
+
+extern "C" int mq_gather_qmm(const MqGatherArgs *args, void *stream) {
+  if (args == nullptr) return fail(MQ_ERR_INVALID, "args is NULL");
+  const MqGatherArgs &a = *args;
+  if (a.x == nullptr || a.routes == nullptr || a.out == nullptr) return fail(MQ_ERR_INVALID, "x, routes and out are required");
+  if (a.group_size != 32 && a.group_size != 64) return fail(MQ_ERR_INVALID, "group_size must be 32 or 64");
+  if (a.in_width == 0 || a.in_width % kKS)
+    return fail(MQ_ERR_UNSUPPORTED, "gather_qmm needs in_width a positive multiple of %u (got %u)", kKS, a.in_width);
+  if (a.out_width == 0 || a.out_width % 4u)
+    return fail(MQ_ERR_UNSUPPORTED, "gather_qmm needs out_width a positive multiple of 4 (got %u)", a.out_width);
+  if (a.in_width > MQ_MAX_WIDTH || a.out_width > MQ_MAX_WIDTH) return fail(MQ_ERR_INVALID, "width out of bounds");
+  if (a.x_rows == nullptr && a.x_count < a.rows)
+    return fail(MQ_ERR_INVALID, "without x_rows, x must hold every row (x_count %u < rows %u)", a.x_count, a.rows);
+  if (static_cast<uint64_t>(a.x_count) * a.in_width * 2u >= (1ull << 31) || a.rows >= (1u << 28))
+    return fail(MQ_ERR_UNSUPPORTED, "x must stay below 2 GiB and rows below 2^28");
+  int rc;
+  if ((rc = validate_proj_grouped(a.w, "w"))) return rc;
+  if (a.rows == 0) return MQ_OK;
+  KeySpace ks;
+  ks.slots = a.w.pool != nullptr ? a.w.pool_slots : 0u;
+  ks.ids = a.w.stream_pack != nullptr ? a.w.stream_records : (a.w.weight != nullptr ? a.expert_count : 0u);
+  const GatherLayout l = make_gather_layout(a.rows, ks.slots + ks.ids);
+  if (a.workspace == nullptr || a.workspace_bytes < l.total)
+    return fail(MQ_ERR_INVALID, "workspace needs %llu bytes (got %llu)", static_cast<unsigned long long>(l.total),
+                static_cast<unsigned long long>(a.workspace_bytes));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  unsigned int *err = nullptr;
+  if ((rc = device_flags_grouped(&err, s))) return rc;
+  uint8_t *ws = static_cast<uint8_t *>(a.workspace);
+  uint32_t *order = reinterpret_cast<uint32_t *>(ws + l.order);
+  GroupTile *tiles = reinterpret_cast<GroupTile *>(ws + l.tiles);
+  uint32_t *n_tiles = reinterpret_cast<uint32_t *>(ws + l.n_tiles);
+  const SortBufs sb{reinterpret_cast<uint32_t *>(ws + l.counts), reinterpret_cast<uint32_t *>(ws + l.cursor),
+                    reinterpret_cast<uint32_t *>(ws + l.row_key), order, tiles, n_tiles};
+  if ((rc = sort_rows(a.routes, a.rows, a.rows, ks, sb, err, s))) return rc;
+  const uint32_t *xmap = order;  // without x_rows, sorted row i reads x row order[i]
+  if (a.x_rows != nullptr) {
+    uint32_t *m = reinterpret_cast<uint32_t *>(ws + l.xmap);
+    hipLaunchKernelGGL(gather_map_kernel, dim3(ceil_div(a.rows, 256)), dim3(256), 0, s, order, a.x_rows, a.rows,
+                       a.x_count, m, err);
+    if ((rc = check_launch("gather_map_kernel"))) return rc;
+    xmap = m;
+  }
+  uint32_t resident = 0;
+  if ((rc = gemm_blocks(&resident))) return rc;
+  GemmParams gp{};
+  gp.x = a.x;
+  gp.x_bytes = a.x_count * a.in_width * 2u;
+  gp.xmap = xmap;
+  gp.xmap_bytes = a.rows * 4u;
+  gp.w0 = a.w;
+  gp.tiles = tiles;
+  gp.tiles_bytes = l.max_tiles * static_cast<uint32_t>(sizeof(GroupTile));
+  gp.n_tiles = n_tiles;
+  gp.order = order;
+  gp.order_bytes = a.rows * 4u;
+  gp.out = a.out;
+  gp.slots = 1u;
+  gp.routed_rows = a.rows;
+  gp.K = a.in_width;
+  gp.N = a.out_width;
+  gp.dense_count = a.expert_count;
+  gp.err = err;
+  const uint32_t items = l.max_tiles * ceil_div(a.out_width, kDownFeatures);
+  return launch_gemm<kModeGather>(gp, a.group_size, std::min(ceil_div(items, 8) * 8u, resident), s);
+}
 
 extern "C" int mq_moe_grouped(const MqGroupedArgs *args, void *stream) {
   if (args == nullptr) return fail(MQ_ERR_INVALID, "args is NULL");

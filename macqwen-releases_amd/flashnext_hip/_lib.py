@@ -24,6 +24,8 @@ MQ_SLOT_BIT = 0x80000000
 MQ_DECODE_RETURN_ALL = 1
 MQ_DECODE_UNFUSED_UP = 2
 MQ_SWIGLU_SCALAR = 1
+MQ_DEVFLAG_BAD_ROUTE = 1
+MQ_DEVFLAG_BAD_ROW = 2
 
 # Every symbol the header declares (checked by the CPU test suite).
 EXPORTS = (
@@ -32,7 +34,8 @@ EXPORTS = (
     "mq_q4_unpack", "mq_q4_dequant", "mq_q4_qmv", "mq_gather_qmv",
     "mq_swiglu", "mq_sigmoid", "mq_bf16_round_check",
     "mq_route_topk", "mq_moe_decode", "mq_moe_layer", "mq_grouped_workspace_size",
-    "mq_moe_grouped", "mq_moe_grouped_static", "mq_pool_refill_async",
+    "mq_moe_grouped", "mq_moe_grouped_static", "mq_gather_qmm_workspace_size", "mq_gather_qmm",
+    "mq_pool_refill_async",
 )
 
 
@@ -144,6 +147,24 @@ class MqGroupedArgs(ctypes.Structure):
     ]
 
 
+class MqGatherArgs(ctypes.Structure):
+    _fields_ = [
+        ("x", ctypes.c_void_p),
+        ("x_rows", ctypes.c_void_p),
+        ("routes", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("w", MqProjection),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_uint64),
+        ("x_count", ctypes.c_uint32),
+        ("rows", ctypes.c_uint32),
+        ("in_width", ctypes.c_uint32),
+        ("out_width", ctypes.c_uint32),
+        ("expert_count", ctypes.c_uint32),
+        ("group_size", ctypes.c_uint32),
+    ]
+
+
 _LIB = None
 _LOAD_ERROR: str | None = None
 
@@ -172,6 +193,8 @@ def _declare(lib) -> None:
         "mq_grouped_workspace_size": ([u32, u32, u32, u32, u32, i32], u64),
         "mq_moe_grouped": ([c.POINTER(MqGroupedArgs), vp], i32),
         "mq_moe_grouped_static": ([c.POINTER(MqGroupedArgs), vp], i32),
+        "mq_gather_qmm_workspace_size": ([u32, u32], u64),
+        "mq_gather_qmm": ([c.POINTER(MqGatherArgs), vp], i32),
         "mq_pool_refill_async": ([vp, u64, u64, u32, vp, vp, u32, u64, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
@@ -195,7 +218,7 @@ def load(path: str | os.PathLike | None = None):
         _LOAD_ERROR = f"cannot load {target}: {exc}"
         raise NativeUnavailable(_LOAD_ERROR) from exc
     _declare(lib)
-    for which, struct in enumerate((MqProjection, MqMoeArgs, MqRouteArgs, MqGroupedArgs)):
+    for which, struct in enumerate((MqProjection, MqMoeArgs, MqRouteArgs, MqGroupedArgs, MqGatherArgs)):
         native = int(lib.mq_abi_struct_size(which))
         if native != ctypes.sizeof(struct):
             _LOAD_ERROR = (f"{target} is out of date: sizeof({struct.__name__}) is {native} in the "

@@ -8,6 +8,7 @@ affine 4-bit format the reference uses (``transpose=True``, ``bits=4``,
 """
 from __future__ import annotations
 
+import ctypes
 import math
 
 import torch
@@ -117,14 +118,29 @@ def dense_projection(weight, scales, biases) -> "_lib.MqProjection":
     return p
 
 
+# Row count from which bf16 gather calls run as grouped MFMA GEMMs over rows
+# sorted by expert; below it, each row is a GEMV.  The reference sorts from
+# the same size (`indices.size >= 64`, models/flashnext/expert_cache.py:1793).
+GROUPED_MIN_ROWS = 64
+
+
 def gather_qmm(x, w, scales, biases, lhs_indices=None, rhs_indices=None, transpose: bool = True,
                group_size: int = 32, bits: int = 4, mode: str = "affine",
                sorted_indices: bool = False) -> torch.Tensor:
     """``mx.gather_qmm``: ``out[b] = x[lhs[b]] @ dequant(w[rhs[b]]).T``.
 
-    ``x``: ``[*Bx, M, K]``; ``w``: ``[E, N, K/8]``; indices broadcast with the
-    batch shape.  Returns ``[*B, M, N]`` in x's dtype.  ``sorted_indices`` is a
-    scheduling hint that does not change any value.
+    ``x``: ``[*Bx, M, K]``; ``w``: ``[E, N, K/8]``.  As in MLX, ``lhs_indices``
+    defaults to every batch of x and ``rhs_indices`` to every expert, and the
+    two broadcast to the output batch.  Returns ``[*B, M, N]`` in x's dtype.
+    ``sorted_indices`` is a scheduling hint that does not change any value.
+
+    bf16 calls of at least ``GROUPED_MIN_ROWS`` rows with K a multiple of 128
+    (the prefill / verify shape: x ``[T*k, 1, H]`` after the sort,
+    models/flashnext/expert_cache.py:787-810, 1790-1806) run as one grouped
+    MFMA GEMM (``mq_gather_qmm``); the rest run one GEMV per row
+    (``mq_gather_qmv``).  Neither path copies x per row or waits for the
+    device: an expert index outside the bank raises a device flag that
+    ``check_device_errors()`` reports, and its row reads zero weights.
     """
     _check_format(bits, group_size, mode, transpose)
     x = require_cuda(x, "x")
@@ -137,30 +153,56 @@ def gather_qmm(x, w, scales, biases, lhs_indices=None, rhs_indices=None, transpo
     experts, n, k = w.shape[0], w.shape[1], w.shape[2] * 8
     if x.dim() < 2 or x.shape[-1] != k:
         raise ValueError("x must be [..., M, K] with K matching the weights")
+    if s.shape != (experts, n, k // group_size) or b.shape != s.shape:
+        raise ValueError("scales/biases do not match the packed weight shape")
+    dev = x.device
     m = x.shape[-2]
-    bx = x.shape[:-2]
-    if lhs_indices is not None:
-        lhs = require_cuda(lhs_indices, "lhs_indices").to(torch.int64)
-        flat_x = x.reshape(-1, m, k)
-        x = flat_x[lhs.reshape(-1)].reshape(lhs.shape + (m, k))
-        bx = lhs.shape
-    if rhs_indices is None:
-        rhs = torch.arange(experts, device=x.device)[: max(1, int(math.prod(bx)))].reshape(bx) \
-            if len(bx) else torch.zeros((), dtype=torch.int64, device=x.device)
-    else:
-        rhs = require_cuda(rhs_indices, "rhs_indices")
-    batch = torch.broadcast_shapes(tuple(bx), tuple(rhs.shape))
-    xb = x.expand(batch + (m, k)).contiguous()
-    rb = rhs.to(torch.int64).expand(batch).reshape(-1)
-    if rb.numel() and (int(rb.min()) < 0 or int(rb.max()) >= experts):
-        raise ValueError("rhs_indices contain an expert outside the weight bank")
-    routes = rb.repeat_interleave(m).to(torch.int32).contiguous()
-    pairs = routes.numel()
-    out = torch.empty(batch + (m, n), dtype=x.dtype, device=x.device)
-    if pairs == 0:
+    bx = tuple(x.shape[:-2])
+    x_batches = int(math.prod(bx))
+    lhs = (torch.arange(x_batches, device=dev).reshape(bx) if lhs_indices is None
+           else require_cuda(lhs_indices, "lhs_indices"))
+    rhs = (torch.arange(experts, device=dev) if rhs_indices is None
+           else require_cuda(rhs_indices, "rhs_indices"))
+    batch = torch.broadcast_shapes(tuple(lhs.shape), tuple(rhs.shape))
+    out = torch.empty(batch + (m, n), dtype=x.dtype, device=dev)
+    rows = int(math.prod(batch)) * m
+    if rows == 0:
         return out
+    if rows >= 2 ** 31:
+        raise ValueError("too many rows")
+    # Route word of every output row (b, j): rhs[b], as int32 (an index
+    # outside [0, experts) becomes a word that addresses nothing).
+    routes = rhs.expand(batch).reshape(-1, 1).expand(-1, m).to(torch.int32).contiguous()
+    # x row of every output row: lhs[b] * M + j, unless that is the identity.
+    identity = lhs_indices is None and tuple(batch) == bx
+    x_rows = None
+    if not identity:
+        x_rows = (lhs.expand(batch).reshape(-1, 1).to(torch.int64) * m
+                  + torch.arange(m, device=dev)).to(torch.int32).reshape(-1)
     proj = dense_projection(w, s, b)
     lib = _lib.load()
-    _lib.check(lib.mq_gather_qmv(ptr(xb), dt, 1, proj, ptr(routes), ptr(out), pairs, 1, k, n,
+    x2 = x.reshape(-1, k)
+    if dt == _lib.MQ_BF16 and rows >= GROUPED_MIN_ROWS and k % 128 == 0 and n % 4 == 0:
+        a = _lib.MqGatherArgs()
+        a.x, a.x_rows, a.routes, a.out = ptr(x2), ptr(x_rows), ptr(routes), ptr(out)
+        a.w = proj
+        a.x_count, a.rows, a.in_width, a.out_width = x2.shape[0], rows, k, n
+        a.expert_count, a.group_size = experts, group_size
+        ws_bytes = int(lib.mq_gather_qmm_workspace_size(rows, experts))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws_bytes
+        _lib.check(lib.mq_gather_qmm(ctypes.byref(a), stream_handle()), lib)
+        return out
+    # GEMV per row: x is read as [tokens, in] with `slots` rows per token
+    # when the rows of one x row are consecutive (the decode shape x
+    # [T, 1, 1, H] against indices [T, k]); otherwise the rows are gathered.
+    tokens, slots, xs = rows, 1, x2
+    bxp = (1,) * (len(batch) - len(bx)) + bx
+    if not identity:
+        if m == 1 and lhs_indices is None and len(batch) and bxp[-1] == 1 and bxp[:-1] == tuple(batch[:-1]):
+            tokens, slots = x_batches, batch[-1]
+        else:
+            xs = x2.index_select(0, x_rows.to(torch.int64))
+    _lib.check(lib.mq_gather_qmv(ptr(xs), dt, 0, ctypes.byref(proj), ptr(routes), ptr(out), tokens, slots, k, n,
                                  experts, group_size, stream_handle()), lib)
     return out

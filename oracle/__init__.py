@@ -28,6 +28,8 @@ PINNING = {
     "bf16.f64_to_bf16": "brute force vs exact rational rounding (fractions) on random + tie inputs",
     "q4.pack_q4/unpack_q4": "reference packing loop test_metal_runtime_g64.py:16-26; round trip; hand KAT",
     "q4.qmv": "closed form (scales=1,biases=0 integer dot; affine linearity) + brute force vs fractions",
+    "q4.gather_qmm": "closed form (scales=1, biases=0 integer dots per row's own expert) + row-permutation "
+                     "equivariance; rows are q4.ExpertBank.project, whose weights are pinned below",
     "router.softmax_topk": "brute force sort on tiny inputs; tie order; closed-form softmax values",
     "router.renorm": "closed form bf16 arithmetic on hand-computed cases",
     "router.keep_for_mass": "hand KAT of adaptive_topk.py:43-50 semantics",

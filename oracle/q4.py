@@ -170,11 +170,14 @@ class ExpertBank:
         return np.asarray(x_f, dtype=np.float64) @ w.T
 
 
-def gather_qmm(x_bits, bank: ExpertBank, rhs_indices) -> np.ndarray:
+def gather_qmm(x_bits, bank: ExpertBank, rhs_indices, weights: str = "exact") -> np.ndarray:
     """MLX ``gather_qmm(x, w, s, b, rhs_indices, transpose=True)`` for 2-D rows.
 
     ``x_bits``: bf16 ``[N, K]`` (one row per gathered product);
-    ``rhs_indices``: ``[N]`` expert ids.  Returns bf16 ``[N, O]``.  Sorting the
+    ``rhs_indices``: ``[N]`` expert ids.  Returns bf16 ``[N, O]``, each row
+    ``bf16(x_row . W_e)`` with the dot product in float64 over the exact
+    dequantized weights (``weights="exact"``) or over the weights rounded to
+    bf16 first (``"bf16"``, the MFMA tiles of the grouped GEMM).  Sorting the
     rows (``sorted_indices=True``) does not change any row's value.
     """
     x = bf16_to_f32(x_bits).astype(np.float64)
@@ -182,5 +185,5 @@ def gather_qmm(x_bits, bank: ExpertBank, rhs_indices) -> np.ndarray:
     out = np.empty((idx.size, bank.out_width), dtype=np.float64)
     for e in np.unique(idx):
         rows = np.nonzero(idx == e)[0]
-        out[rows] = bank.project(x[rows], int(e))
+        out[rows] = bank.project(x[rows], int(e), weights)
     return f64_to_bf16(out)

@@ -86,6 +86,34 @@ def test_qmv_integer_closed_form():
     assert np.array_equal(got, x @ q.T.astype(np.float64))
 
 
+def test_gather_qmm_integer_closed_form_and_row_order():
+    """gather_qmm row r = bf16(x_r . W_{e_r}) with each row's own expert: with
+    scales 1 and biases 0 the products are integer dots, exact in bf16 when
+    small; every expert's rows differ (distinct weights), so a row sent to
+    the wrong expert or a transposed operand fails; permuting the rows
+    permutes the outputs; both weight modes agree on bf16-exact weights."""
+    rng = np.random.default_rng(6)
+    experts, n, k = 5, 6, 64
+    q = rng.integers(0, 16, (experts, n, k), dtype=np.uint8)
+    packed = q4.pack_q4(q)
+    ones = np.full((experts, n, k // 32), 0x3F80, dtype=np.uint16)
+    zeros = np.zeros((experts, n, k // 32), dtype=np.uint16)
+    bank = q4.ExpertBank(packed, ones, zeros, 32)
+    # x in [-2, 2] on the first 8 inputs, 0 elsewhere: |dot| <= 2*15*8 = 240 < 256,
+    # so every integer result is exact in bf16's 8-bit significand
+    x = np.zeros((23, k), dtype=np.float32)
+    x[:, :8] = rng.integers(-2, 3, (23, 8))
+    idx = rng.integers(0, experts, 23)
+    got = bf16.bf16_to_f32(q4.gather_qmm(bf16.f32_to_bf16(x), bank, idx)).astype(np.float64)
+    want = np.stack([x[r].astype(np.float64) @ q[idx[r]].T.astype(np.float64) for r in range(23)])
+    assert np.array_equal(got, want)
+    perm = rng.permutation(23)
+    got_p = q4.gather_qmm(bf16.f32_to_bf16(x[perm]), bank, idx[perm])
+    assert np.array_equal(got_p, q4.gather_qmm(bf16.f32_to_bf16(x), bank, idx)[perm])
+    assert np.array_equal(q4.gather_qmm(bf16.f32_to_bf16(x), bank, idx, "bf16"),
+                          q4.gather_qmm(bf16.f32_to_bf16(x), bank, idx))
+
+
 def test_qmv_affine_linearity_and_group64():
     rng = np.random.default_rng(4)
     k, n = 128, 5
