@@ -483,12 +483,88 @@ __device__ __forceinline__ void load_groups(uint32_t &s, uint32_t &b, const WRow
   }
 }
 
-template <int G>
+template <int G, bool GROUPS = true>
 __device__ __forceinline__ void load_wstage(WStage &r, const WRow &wr, uint32_t K, uint32_t stage, uint32_t half) {
   const uint32_t off_w = wstage_off(wr, K, stage, half);
   r.w[0] = buf_load16(wr.e.w, off_w);
   r.w[1] = buf_load16(wr.e.w, off_w + 32u);
-  load_groups<G>(r.s, r.b, wr, K, stage, half);
+  if constexpr (GROUPS) load_groups<G>(r.s, r.b, wr, K, stage, half);
+}
+
+// Group windows: when the stage count allows, the scales and biases are
+// fetched W = 2 or 4 stages at a time.  Lane (row, half) loads the groups of
+// stages stage0 + half * W / 2 .. + W / 2 - 1 of its row, so one load
+// instruction per array covers W stages of the wave's 32 rows in 8 W
+// contiguous bytes each (group 32; 4 W with group 64), and v_permlane32_swap
+// then hands each half the other half's stages.  Small scattered loads are
+// what limits the stream here: every row's scales sit in their own cache
+// line, and per-stage 8-byte loads spend as many L1 tag lookups and miss
+// slots as the weights themselves.
+template <int G, int W>
+struct GroupWindow {
+  static constexpr int kWords = W * (kKS / G) / 4;  // 32-bit words per lane and array
+  uint32_t s[kWords], b[kWords];                     // as loaded: this half's stages
+};
+
+template <int G, int W>
+__device__ __forceinline__ void load_window(GroupWindow<G, W> &r, const WRow &wr, uint32_t K, uint32_t stage0,
+                                            uint32_t half) {
+  constexpr int kWords = GroupWindow<G, W>::kWords;
+  const uint32_t g0 = wr.row * (K / G) + (stage0 + half * (W / 2)) * (kKS / G);
+  const int o = static_cast<int>(wr.ok ? g0 * 2u : kOutOfRange);
+  if constexpr (kWords == 4) {
+    const u32x4_t sv = __builtin_amdgcn_raw_buffer_load_b128(wr.e.s, o, 0, 0);
+    const u32x4_t bv = __builtin_amdgcn_raw_buffer_load_b128(wr.e.b, o, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      r.s[q] = sv[q];
+      r.b[q] = bv[q];
+    }
+  } else if constexpr (kWords == 2) {
+    const u32x2_t sv = __builtin_amdgcn_raw_buffer_load_b64(wr.e.s, o, 0, 0);
+    const u32x2_t bv = __builtin_amdgcn_raw_buffer_load_b64(wr.e.b, o, 0, 0);
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      r.s[q] = sv[q];
+      r.b[q] = bv[q];
+    }
+  } else {
+    r.s[0] = buf_load4(wr.e.s, static_cast<uint32_t>(o));
+    r.b[0] = buf_load4(wr.e.b, static_cast<uint32_t>(o));
+  }
+}
+
+// The lane's (scale, bias) bf16 pairs for stages stage0 .. stage0 + W - 1
+// from an arrived window (the pair layout of load_groups).
+template <int G, int W>
+__device__ __forceinline__ void open_window(const GroupWindow<G, W> &r, uint32_t half, uint32_t (&sp)[W],
+                                            uint32_t (&bp)[W]) {
+  constexpr int kWords = GroupWindow<G, W>::kWords;
+  // v_permlane32_swap(x, x): the first result holds lanes 0-31's value in
+  // both halves (the window's first W / 2 stages), the second lanes 32-63's.
+  uint32_t sw[2][kWords], bw[2][kWords];
+#pragma unroll
+  for (int q = 0; q < kWords; ++q) {
+    const auto sx = __builtin_amdgcn_permlane32_swap(r.s[q], r.s[q], false, false);
+    const auto bx = __builtin_amdgcn_permlane32_swap(r.b[q], r.b[q], false, false);
+    sw[0][q] = sx[0];
+    sw[1][q] = sx[1];
+    bw[0][q] = bx[0];
+    bw[1][q] = bx[1];
+  }
+  constexpr int kPerStage = kKS / G / 2;  // words per stage: 2 (group 32) or 1 (group 64)
+#pragma unroll
+  for (int st = 0; st < W; ++st) {
+    const int h = st / (W / 2), w0 = (st % (W / 2)) * kPerStage;
+    if constexpr (G == 32) {
+      const uint32_t sel = half ? 0x07060302u : 0x05040100u;  // groups (half, half + 2) of the stage's four
+      sp[st] = __builtin_amdgcn_perm(sw[h][w0 + 1], sw[h][w0], sel);
+      bp[st] = __builtin_amdgcn_perm(bw[h][w0 + 1], bw[h][w0], sel);
+    } else {
+      sp[st] = sw[h][w0];
+      bp[st] = bw[h][w0];
+    }
+  }
 }
 
 // A thread's share of the activation tile of one stage: kXChunks 16-byte
@@ -538,13 +614,13 @@ __device__ __forceinline__ void mma_step(f32x16_t (&acc)[4], bf16x8_t (&bq)[4], 
 // cursor's stage as soon as each part of it has been consumed (scales and
 // biases first, then the first and second four words), so that a slot's
 // registers are never live twice.
-template <int G, int NSLAB>
+template <int G, int NSLAB, bool GROUPS>
 __device__ __forceinline__ void stage_mma(f32x16_t (&acc)[4], const uint16_t *xl, WStage &w, const WRow &lw,
-                                          uint32_t K, uint32_t ls, uint32_t half) {
-  const float s0 = __uint_as_float(w.s << 16), b0 = __uint_as_float(w.b << 16);
-  const float s1 = __uint_as_float(w.s & 0xffff0000u), b1 = __uint_as_float(w.b & 0xffff0000u);
+                                          uint32_t K, uint32_t ls, uint32_t half, uint32_t sp, uint32_t bp) {
+  const float s0 = __uint_as_float(sp << 16), b0 = __uint_as_float(bp << 16);
+  const float s1 = __uint_as_float(sp & 0xffff0000u), b1 = __uint_as_float(bp & 0xffff0000u);
   const uint32_t off_w = wstage_off(lw, K, ls, half);
-  load_groups<G>(w.s, w.b, lw, K, ls, half);
+  if constexpr (GROUPS) load_groups<G>(w.s, w.b, lw, K, ls, half);
   // Software pipeline over the eight k16 steps: the A operand of step j+1 is
   // dequantized while the MFMAs of step j run; a scheduling barrier per step
   // keeps the compiler from hoisting further ahead (which only adds live
@@ -781,9 +857,16 @@ __device__ __forceinline__ void down_epilogue(const f32x16_t (&acc)[4], const It
 // Pipeline state carried across stages and items: the weight ring, the load
 // cursor (row and stage, NS stages ahead of compute), and the activation
 // registers of the next stage with their source rows.
-template <int MODE, int NS, int G>
+template <int MODE, int NS, int G, int W>
 struct Pipe {
+  // W stages per group window (W = 2 or 4, NS == 2, W divides the stage
+  // count); W = 1: the groups ride in the ring slots.  The stage loop is
+  // unrolled by U = max(NS, W) stages, so every window starts at u = 0.
+  static constexpr bool kWindow = W > 1;
+  static constexpr int U = NS > W ? NS : W;
   WStage ring[NS];
+  GroupWindow<G, kWindow ? W : 2> win;  // the next window, loaded W - NS stages before it opens
+  uint32_t wsp[kWindow ? W : 1], wbp[kWindow ? W : 1];  // the open window's pairs
   WRow lw;
   uint32_t ls;
   XStage xv;
@@ -798,17 +881,25 @@ struct Pipe {
     const uint32_t half = static_cast<uint32_t>(lane) >> 5;
     const uint32_t xrow = static_cast<uint32_t>(tid) / kXParts, xpart = static_cast<uint32_t>(tid) % kXParts;
     const uint32_t xl_off = (static_cast<uint32_t>(lane) & 31u) * kXRow + 32u * half;
-    for (uint32_t s0 = 0; s0 < S; s0 += NS) {
+    for (uint32_t s0 = 0; s0 < S; s0 += U) {
 #pragma unroll
-      for (int u = 0; u < NS; ++u) {
+      for (int u = 0; u < U; ++u) {
         const uint32_t s = s0 + u;
         uint16_t *xb = xs + (s & 1u) * kXTile;
         if (xrow < 32u * NSLAB) store_xstage(xb, xv, xrow, xpart);  // rows past the active slabs are never read
         __syncthreads();
-        const bool last = u == NS - 1 && s + 1u == S;
+        const bool last = u == U - 1 && s + 1u == S;
         if (last) xsrc_next = x_source<MODE>(n, p, tid);
         load_xstage(xv, xr, last ? xsrc_next : xsrc, p.K, last ? 0u : s + 1u, xpart);
-        stage_mma<G, NSLAB>(acc, xb + xl_off, ring[u], lw, p.K, ls, half);
+        if constexpr (kWindow) {
+          if (u == 0) open_window<G, W>(win, half, wsp, wbp);  // stages s .. s + W - 1
+          // The load cursor (NS stages ahead) reaches the next window's first stage.
+          if (u == W - NS) load_window<G, W>(win, lw, p.K, ls, half);
+          stage_mma<G, NSLAB, false>(acc, xb + xl_off, ring[u % NS], lw, p.K, ls, half, wsp[u], wbp[u]);
+        } else {
+          stage_mma<G, NSLAB, true>(acc, xb + xl_off, ring[u % NS], lw, p.K, ls, half, ring[u % NS].s,
+                                    ring[u % NS].b);
+        }
         if (++ls == S) {
           // The load cursor finished an item.  With NS == S it was already
           // in the next item n, and this is compute's last stage of c.
@@ -829,7 +920,7 @@ struct Pipe {
 // the next item start while the current one finishes (NS <= stages per item,
 // so the load cursor is at most one item ahead), and tile records and sorted
 // rows are fetched two items ahead.
-template <int MODE, int NS, int G>
+template <int MODE, int NS, int G, int W>
 __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmParams p) {
   __shared__ __align__(16) uint16_t xs[2 * kXTile];
   constexpr uint32_t kFeat = MODE == kModeGateUp ? kGateUpFeatures : kDownFeatures;
@@ -855,12 +946,17 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmParam
   fetch_rows<MODE>(n, orr, xmr, tid);
 
   // Load cursor: NS stages ahead of the compute cursor.
-  Pipe<MODE, NS, G> pp;
+  Pipe<MODE, NS, G, W> pp;
   pp.lw = weight_row<MODE, G>(c, p, it, nb_count, wave, lane);
   pp.ls = 0;
 #pragma unroll
   for (int u = 0; u < NS; ++u) {
-    load_wstage<G>(pp.ring[u], pp.lw, p.K, pp.ls, half);
+    if constexpr (Pipe<MODE, NS, G, W>::kWindow) {
+      if (u == 0) load_window<G>(pp.win, pp.lw, p.K, pp.ls, half);
+      load_wstage<G, false>(pp.ring[u], pp.lw, p.K, pp.ls, half);
+    } else {
+      load_wstage<G>(pp.ring[u], pp.lw, p.K, pp.ls, half);
+    }
     if (++pp.ls == S) {
       pp.ls = 0;
       pp.lw = weight_row<MODE, G>(n, p, it, nb_count, wave, lane);
@@ -980,12 +1076,12 @@ int validate_proj_grouped(const MqProjection &p, const char *name) {
 // compute cursor.  Two stages ahead keep the kernel within 256 registers per
 // lane with the B-fragment read-ahead (four stages spill; measured on the
 // 4096-token chunk: 4 stages 918-928 us, 2 stages 897-909 us per call).
-template <int MODE, int NS>
+template <int MODE, int NS, int W>
 int launch_gemm_ns(const GemmParams &p, uint32_t group, uint32_t grid, hipStream_t s) {
   if (group == 32)
-    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NS, 32>), dim3(grid), dim3(kGemmThreads), 0, s, p);
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NS, 32, W>), dim3(grid), dim3(kGemmThreads), 0, s, p);
   else
-    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NS, 64>), dim3(grid), dim3(kGemmThreads), 0, s, p);
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE, NS, 64, W>), dim3(grid), dim3(kGemmThreads), 0, s, p);
   return check_launch(MODE == kModeGateUp ? "grouped_gemm_kernel (gate/up)"
                       : MODE == kModeDown ? "grouped_gemm_kernel (down)"
                                           : "grouped_gemm_kernel (gather)");
@@ -994,9 +1090,10 @@ int launch_gemm_ns(const GemmParams &p, uint32_t group, uint32_t grid, hipStream
 template <int MODE>
 int launch_gemm(const GemmParams &p, uint32_t group, uint32_t grid, hipStream_t s) {
   const uint32_t stages = p.K / kKS;
-  if (stages % 2 == 0) return launch_gemm_ns<MODE, 2>(p, group, grid, s);
-  if (stages % 3 == 0) return launch_gemm_ns<MODE, 3>(p, group, grid, s);
-  return launch_gemm_ns<MODE, 1>(p, group, grid, s);
+  if (stages % 4 == 0) return launch_gemm_ns<MODE, 2, 4>(p, group, grid, s);
+  if (stages % 2 == 0) return launch_gemm_ns<MODE, 2, 2>(p, group, grid, s);
+  if (stages % 3 == 0) return launch_gemm_ns<MODE, 3, 1>(p, group, grid, s);
+  return launch_gemm_ns<MODE, 1, 1>(p, group, grid, s);
 }
 
 KeySpace key_space(const MqGroupedArgs &a) {
