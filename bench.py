@@ -201,6 +201,7 @@ def prefill_bench(torch, dev, reps: int = 24, warm: int = 48, layers: int = 4) -
     counts = np.bincount(inds.reshape(-1), minlength=EXPERTS)
     out, y = gs[0](x, routes, scores)
     check = prefill_check(torch, stacks[0], x, inds, scores, out, y, counts)
+    chain = gather_chain_bench(torch, dev, stacks, x, inds, reps=reps // 2, warm=warm // 2)
     del stacks, gs
     return {"workload": f"{T} tokens x top-{TOP_K}, {EXPERTS} experts, Zipf(1.1) rows "
                         f"(max {int(counts.max())}, median {int(np.median(counts))}, min {int(counts.min())}), "
@@ -209,7 +210,49 @@ def prefill_bench(torch, dev, reps: int = 24, warm: int = 48, layers: int = 4) -
             "mfma_frac": round(tflops / BF16_PEAK_TFLOPS, 4),
             "note": (f"sort + grouped MFMA GEMMs + bf16 combine timed together over {reps} calls after {warm} "
                      "untimed ones (sustained chunk rate); routed experts only"),
-            "check": check}
+            "check": check, "gather_qmm_chain": chain}
+
+
+def gather_chain_bench(torch, dev, stacks, x, inds, reps: int, warm: int) -> dict:
+    """The reference's per-projection prefill chain on the same chunk, through
+    the drop-in op: rows sorted by expert (x[T*k, 1, H]), then gather_qmm for
+    gate and up, swiglu, gather_qmm for down (models/flashnext/expert_cache.py:
+    1790-1806), each layer's banks in turn.  The sort and row gather happen
+    before the timed region, as in the reference's _gather_sort."""
+    import numpy as np
+
+    from flashnext_hip import ops
+
+    T = x.shape[0]
+    flat = inds.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    xs = x.index_select(0, torch.from_numpy(order // TOP_K).to(dev)).reshape(T * TOP_K, 1, HIDDEN)
+    rhs = torch.from_numpy(flat[order].astype(np.int64)).to(dev)
+
+    def chain(banks):
+        gate, up, down = banks
+        g = ops.gather_qmm(xs, gate.weight, gate.scales, gate.biases, rhs_indices=rhs, sorted_indices=True)
+        u = ops.gather_qmm(xs, up.weight, up.scales, up.biases, rhs_indices=rhs, sorted_indices=True)
+        return ops.gather_qmm(ops.swiglu(g, u), down.weight, down.scales, down.biases, rhs_indices=rhs,
+                              sorted_indices=True)
+
+    for i in range(warm):
+        chain(stacks[i % len(stacks)])
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(3):  # median of three timed blocks
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(reps):
+            chain(stacks[i % len(stacks)])
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) / reps)
+    ms = sorted(times)[1]
+    flops = 2.0 * T * TOP_K * 3 * HIDDEN * INTER
+    return {"ops": f"3 x ops.gather_qmm (mq_gather_qmm) + ops.swiglu over {T * TOP_K} sorted rows",
+            "us": round(ms * 1000, 1), "us_blocks": [round(t * 1000, 1) for t in times],
+            "tflops": round(flops / (ms * 1e-3) / 1e12, 1)}
 
 
 def prefill_check(torch, banks, x, inds, scores, out, y, counts) -> dict:
