@@ -233,11 +233,14 @@ int mq_gather_qmv(const void *x, int x_dtype, int slot_input, const MqProjection
  * unfused up path calls it (models/flashnext/metal_runtime.py:895-907), with
  * the fused Up epilogue's rounding points (:278-287): m = |g|, e = T(exp(m)),
  * d = T(1 + e), s = T(1 / d), sig = g < 0 ? s : T(1 - s), out = T(T(g * sig) * u),
- * exp correctly rounded to float32.  bf16 runs take the grouped kernels'
- * four-at-a-time sequence, or with MQ_SWIGLU_SCALAR the decode kernels'
- * per-element sequence (bit-identical by construction; both are exported so
- * either can be checked on its own).  n < 2^31. */
+ * exp correctly rounded to float32.  bf16 runs take the four-at-a-time
+ * sequence, with MQ_SWIGLU_SCALAR the decode kernels'
+ * per-element sequence, or with MQ_SWIGLU_TABLE the grouped gate/up
+ * epilogue's sequence with the sigmoid looked up in a per-block table
+ * (bit-identical by construction; all are exported so each can be checked on
+ * its own).  The two flags exclude each other.  n < 2^31. */
 #define MQ_SWIGLU_SCALAR 1u
+#define MQ_SWIGLU_TABLE 2u
 int mq_swiglu(const void *gate, const void *up, void *out, uint64_t n, int dtype, uint32_t flags,
               void *stream);
 

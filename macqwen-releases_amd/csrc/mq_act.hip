@@ -8,8 +8,9 @@
 // same sigmoid sequence alone (the shared-expert gate, mx.sigmoid in
 // models/flashnext/adaptive_topk.py:264).  Both run the exact device
 // sequences the decode and grouped kernels run (swiglu_bf16 per element,
-// swiglu_bf16_n<4> in runs of four, sigmoid_bf16), so their outputs pin those
-// sequences bit for bit.
+// swiglu_bf16_n<4> in runs of four, with MQ_SWIGLU_TABLE the grouped gate/up
+// epilogue's table-driven swiglu_bf16_tab_n<4>, sigmoid_bf16), so their
+// outputs pin those sequences bit for bit.
 #include <algorithm>
 
 #include "mq_internal.h"
@@ -20,24 +21,32 @@ namespace {
 
 constexpr int kActThreads = 256;
 
-// Four elements per thread.  Runs of four use swiglu_bf16_n<4> (the grouped
-// gate/up epilogue) unless `scalar` selects the per-element sequence (the
-// decode gate/up epilogue and the unfused decode pass); a tail of fewer than
-// four elements always goes one at a time.
+// Four elements per thread.  Runs of four use swiglu_bf16_n<4> unless `seq`
+// selects the per-element sequence (the decode gate/up epilogue and the
+// unfused decode pass) or the table-driven one of the grouped gate/up
+// epilogue (the block fills its LDS table as the grouped kernel does); a
+// tail of fewer than four elements always goes one at a time.
+enum SwigluSeq : int { kSeqRuns = 0, kSeqScalar = 1, kSeqTable = 2 };
+
 __global__ __launch_bounds__(kActThreads) void swiglu_bf16_kernel(const uint16_t *__restrict__ g,
                                                                    const uint16_t *__restrict__ u,
-                                                                   uint16_t *__restrict__ out, uint64_t n,
-                                                                   bool scalar) {
+                                                                   uint16_t *__restrict__ out, uint64_t n, int seq) {
+  __shared__ uint32_t sig_tab[kSigTabEntries];
+  if (seq == kSeqTable) {  // uniform
+    fill_sig_tab(sig_tab, threadIdx.x, kActThreads);
+    __syncthreads();
+  }
   const uint64_t i0 = (static_cast<uint64_t>(blockIdx.x) * kActThreads + threadIdx.x) * 4u;
   if (i0 >= n) return;
-  if (i0 + 4u <= n && !scalar) {
+  if (i0 + 4u <= n && seq != kSeqScalar) {
     float gv[4], uv[4], v[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       gv[e] = bf16_to_f32(g[i0 + e]);
       uv[e] = bf16_to_f32(u[i0 + e]);
     }
-    swiglu_bf16_n<4>(gv, uv, v);
+    if (seq == kSeqTable) swiglu_bf16_tab_n<4>(gv, uv, v, sig_tab);
+    else swiglu_bf16_n<4>(gv, uv, v);
 #pragma unroll
     for (int e = 0; e < 4; ++e) out[i0 + e] = f32_to_bf16(v[e]);
     return;
@@ -97,14 +106,17 @@ extern "C" int mq_swiglu(const void *gate, const void *up, void *out, uint64_t n
                          void *stream) {
   int rc = check_elementwise(gate, up, out, n, dtype);
   if (rc) return rc;
-  if (flags & ~MQ_SWIGLU_SCALAR) return fail(MQ_ERR_INVALID, "unknown flags 0x%x", flags);
+  if (flags & ~(MQ_SWIGLU_SCALAR | MQ_SWIGLU_TABLE)) return fail(MQ_ERR_INVALID, "unknown flags 0x%x", flags);
+  if ((flags & MQ_SWIGLU_SCALAR) && (flags & MQ_SWIGLU_TABLE))
+    return fail(MQ_ERR_INVALID, "MQ_SWIGLU_SCALAR and MQ_SWIGLU_TABLE exclude each other");
   if (n == 0) return MQ_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == MQ_BF16) {
     const uint64_t threads = (n + 3u) / 4u;
     hipLaunchKernelGGL(swiglu_bf16_kernel, dim3(ceil_div(threads, kActThreads)), dim3(kActThreads), 0, s,
                        static_cast<const uint16_t *>(gate), static_cast<const uint16_t *>(up),
-                       static_cast<uint16_t *>(out), n, (flags & MQ_SWIGLU_SCALAR) != 0);
+                       static_cast<uint16_t *>(out), n,
+                       (flags & MQ_SWIGLU_SCALAR) ? kSeqScalar : (flags & MQ_SWIGLU_TABLE) ? kSeqTable : kSeqRuns);
   } else {
     hipLaunchKernelGGL(swiglu_f32_kernel, dim3(ceil_div(n, kActThreads)), dim3(kActThreads), 0, s,
                        static_cast<const float *>(gate), static_cast<const float *>(up), static_cast<float *>(out),

@@ -769,7 +769,9 @@ __device__ __forceinline__ WRow weight_row(const Item &m, const GemmParams &p, c
 // cells, in four runs q of 4 consecutive features.  Gate waves compute runs
 // 0-1 and up waves runs 2-3, each handing the other its bf16 values of the
 // runs the other computes through LDS (the tile buffer just consumed), so all
-// eight waves share the SwiGLU sequence.
+// eight waves share the SwiGLU sequence.  The sigmoid comes from a per-block
+// LDS table of the sequence's |g|-only part, filled once per launch (about 15
+// VALU instructions per cell instead of about 50 for the whole sequence).
 constexpr uint32_t kExchange = 4u * 4u * 64u * 4u;  // bf16 per gate/up wave pair: 4 slabs x 16 values x 64 lanes
 static_assert(kExchange * (kGemmWaves / 2) <= kXTile, "gate/up exchange must fit in one activation tile");
 
@@ -780,7 +782,7 @@ __device__ __forceinline__ uint32_t ex_off(int t, int i, int lane) {  // run i (
 template <bool UP>
 __device__ __forceinline__ void gateup_epilogue_half(const f32x16_t (&acc)[4], uint16_t *ex, const Item &m,
                                                      const GemmParams &p, uint32_t nb, uint32_t fw, int lane,
-                                                     const bool (&slab)[4]) {
+                                                     const bool (&slab)[4], const uint32_t *sig_tab) {
   constexpr int kRun = UP ? 2 : 0;   // first run this wave computes
   constexpr int kGive = UP ? 0 : 2;  // first run this wave hands over
   uint16_t *give = ex + (UP ? kExchange / 2 : 0u);
@@ -817,7 +819,7 @@ __device__ __forceinline__ void gateup_epilogue_half(const f32x16_t (&acc)[4], u
         gv[e] = UP ? other : own;
         uv[e] = UP ? own : other;
       }
-      swiglu_bf16_n<4>(gv, uv, v);
+      swiglu_bf16_tab_n<4>(gv, uv, v, sig_tab);
       if (feat < p.N) *reinterpret_cast<uint2 *>(dst + feat) = make_uint2(pack_bf16(v[0], v[1]), pack_bf16(v[2], v[3]));
     }
   }
@@ -825,11 +827,11 @@ __device__ __forceinline__ void gateup_epilogue_half(const f32x16_t (&acc)[4], u
 
 __device__ __forceinline__ void gateup_epilogue(const f32x16_t (&acc)[4], uint16_t *xb, const Item &m,
                                                 const GemmParams &p, uint32_t nb, uint32_t wave, int lane,
-                                                const bool (&slab)[4]) {
+                                                const bool (&slab)[4], const uint32_t *sig_tab) {
   const uint32_t fw = wave % (kGemmWaves / 2);
   __syncthreads();  // every wave is done reading the tile in xb
-  if (wave >= kGemmWaves / 2) gateup_epilogue_half<true>(acc, xb + fw * kExchange, m, p, nb, fw, lane, slab);
-  else gateup_epilogue_half<false>(acc, xb + fw * kExchange, m, p, nb, fw, lane, slab);
+  if (wave >= kGemmWaves / 2) gateup_epilogue_half<true>(acc, xb + fw * kExchange, m, p, nb, fw, lane, slab, sig_tab);
+  else gateup_epilogue_half<false>(acc, xb + fw * kExchange, m, p, nb, fw, lane, slab, sig_tab);
 }
 
 // Down and gather epilogue: the bf16 outputs go back to the row's `order`
@@ -923,6 +925,7 @@ struct Pipe {
 template <int MODE, int NS, int G, int W>
 __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmParams p) {
   __shared__ __align__(16) uint16_t xs[2 * kXTile];
+  __shared__ uint32_t sig_tab[MODE == kModeGateUp ? kSigTabEntries : 1u];  // gate/up: the SwiGLU sigmoid table
   constexpr uint32_t kFeat = MODE == kModeGateUp ? kGateUpFeatures : kDownFeatures;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -965,6 +968,9 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmParam
   pp.xsrc = x_source<MODE>(c, p, tid);
   pp.xsrc_next = ~0u;
   load_xstage(pp.xv, xr, pp.xsrc, p.K, 0u, xpart);
+  // While the first loads are in flight.  The stage loop's barriers order
+  // these LDS writes before the first epilogue reads them.
+  if constexpr (MODE == kModeGateUp) fill_sig_tab(sig_tab, static_cast<uint32_t>(tid), kGemmThreads);
 
   f32x16_t acc[4];
 #pragma unroll
@@ -986,7 +992,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grouped_gemm_kernel(GemmParam
     }
     // Every item starts on LDS tile 0; its last stage used tile (S - 1) & 1.
     if constexpr (MODE != kModeGateUp) down_epilogue(acc, c, p, nb, wave, lane, slab);
-    else gateup_epilogue(acc, xs + ((S - 1u) & 1u) * kXTile, c, p, nb, wave, lane, slab);
+    else gateup_epilogue(acc, xs + ((S - 1u) & 1u) * kXTile, c, p, nb, wave, lane, slab, sig_tab);
 #pragma unroll
     for (int t = 0; t < 4; ++t)
 #pragma unroll

@@ -100,13 +100,17 @@ __device__ __forceinline__ float swiglu_bf16(float g, float u) {
 // taken together and the rare float64 re-evaluation runs behind one
 // wave-uniform branch, so the N sequences stay free of divergent control flow
 // and interleave.
+//
+// The sigmoid depends on the gate only through m = |g| (s = bf16(1 / d) and
+// om = bf16(1 - s) with d = bf16(1 + bf16(exp(m)))) and the sign, which picks
+// s (g < 0) or om; sigmoid_parts_n is that |g|-only part.
 template <int N>
-__device__ __forceinline__ void swiglu_bf16_n(const float (&g)[N], const float (&u)[N], float (&out)[N]) {
+__device__ __forceinline__ void sigmoid_parts_n(const float (&m)[N], float (&s)[N], float (&om)[N]) {
   float e[N];
   uint32_t redo = 0u;
 #pragma unroll
   for (int i = 0; i < N; ++i) {
-    const float ef = expf(fabsf(g[i]));
+    const float ef = expf(m[i]);
     const int low = static_cast<int>(__float_as_uint(ef) & 0xffffu);
     if (abs(low - 0x8000) <= 4 || !isfinite(ef)) redo |= 1u << i;
     e[i] = round_bf16_hw(ef);
@@ -114,15 +118,81 @@ __device__ __forceinline__ void swiglu_bf16_n(const float (&g)[N], const float (
   if (__ballot(redo != 0u) != 0ull) {
 #pragma unroll
     for (int i = 0; i < N; ++i)
-      if ((redo >> i) & 1u) e[i] = round_bf16(static_cast<float>(exp(static_cast<double>(fabsf(g[i])))));
+      if ((redo >> i) & 1u) e[i] = round_bf16(static_cast<float>(exp(static_cast<double>(m[i]))));
   }
 #pragma unroll
   for (int i = 0; i < N; ++i) {
     const float d = round_bf16_hw(__fadd_rn(1.0f, e[i]));
-    const float s = recip_bf16(d);
-    const float om = round_bf16_hw(__fsub_rn(1.0f, s));
-    const float silu = round_bf16_hw(__fmul_rn(g[i], g[i] < 0.0f ? s : om));
+    s[i] = recip_bf16(d);
+    om[i] = round_bf16_hw(__fsub_rn(1.0f, s[i]));
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void swiglu_bf16_n(const float (&g)[N], const float (&u)[N], float (&out)[N]) {
+  float m[N], s[N], om[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) m[i] = fabsf(g[i]);
+  sigmoid_parts_n<N>(m, s, om);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float silu = round_bf16_hw(__fmul_rn(g[i], g[i] < 0.0f ? s[i] : om[i]));
     out[i] = round_bf16(__fmul_rn(silu, u[i]));
+  }
+}
+
+// Sigmoid table for bf16 gates: one word per |g| (bf16 bits of s in the low
+// half, of om in the high half), made by sigmoid_parts_n itself, so a lookup
+// equals the sequence bit for bit.  Entry 0 serves every |g| below 2^-8
+// (there exp(|g|) < 1 + 2^-8 - 2^-17 rounds to e = 1, the same as at 0);
+// entries 1.. hold the bf16 values 2^-8 <= |g| < 2^7, one per value (15
+// binades of 128).  |g| >= 2^7 (the float32 exponential overflows from about
+// 88.7), infinities and NaN take the full sequence.  7.7 KB, for LDS.
+constexpr uint32_t kSigTabFirst = 0x3b80u;  // bf16 bits of 2^-8
+constexpr uint32_t kSigTabEnd = 0x4300u;    // bf16 bits of 2^7
+constexpr uint32_t kSigTabEntries = kSigTabEnd - kSigTabFirst + 1u;
+
+__device__ __forceinline__ float sig_tab_gate(uint32_t i) {
+  return i == 0u ? 0.0f : __uint_as_float((kSigTabFirst + i - 1u) << 16);
+}
+
+// Fills tab[0 .. kSigTabEntries) with `threads` threads (this one `t`), four
+// entries per thread and round.  The caller synchronizes before any lookup.
+__device__ __forceinline__ void fill_sig_tab(uint32_t *tab, uint32_t t, uint32_t threads) {
+  for (uint32_t i0 = 4u * t; i0 < kSigTabEntries; i0 += 4u * threads) {
+    float m[4], s[4], om[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) m[k] = sig_tab_gate(min(i0 + k, kSigTabEntries - 1u));
+    sigmoid_parts_n<4>(m, s, om);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (i0 + k < kSigTabEntries) tab[i0 + k] = (__float_as_uint(s[k]) >> 16) | (__float_as_uint(om[k]) & 0xffff0000u);
+  }
+}
+
+// swiglu_bf16_n for bf16-valued gates with the sigmoid looked up in `tab`
+// (filled by fill_sig_tab); gates outside the table take swiglu_bf16_n behind
+// one wave-uniform branch.  Bit-identical to swiglu_bf16_n.
+template <int N>
+__device__ __forceinline__ void swiglu_bf16_tab_n(const float (&g)[N], const float (&u)[N], float (&out)[N],
+                                                  const uint32_t *tab) {
+  uint32_t slow = 0u;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const uint32_t b = (__float_as_uint(g[i]) >> 16) & 0x7fffu;  // |g| as bf16 bits
+    if (b >= kSigTabEnd) slow |= 1u << i;
+    const uint32_t c = b < kSigTabEnd ? b : kSigTabEnd - 1u;  // keeps the read in the table
+    const uint32_t w = tab[c >= kSigTabFirst ? c - kSigTabFirst + 1u : 0u];
+    const float sel = __uint_as_float(g[i] < 0.0f ? w << 16 : w & 0xffff0000u);
+    const float silu = round_bf16_hw(__fmul_rn(g[i], sel));
+    out[i] = round_bf16(__fmul_rn(silu, u[i]));
+  }
+  if (__ballot(slow != 0u) != 0ull) {
+    float full[N];
+    swiglu_bf16_n<N>(g, u, full);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if ((slow >> i) & 1u) out[i] = full[i];
   }
 }
 

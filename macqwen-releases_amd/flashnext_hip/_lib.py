@@ -24,6 +24,7 @@ MQ_SLOT_BIT = 0x80000000
 MQ_DECODE_RETURN_ALL = 1
 MQ_DECODE_UNFUSED_UP = 2
 MQ_SWIGLU_SCALAR = 1
+MQ_SWIGLU_TABLE = 2
 MQ_DEVFLAG_BAD_ROUTE = 1
 MQ_DEVFLAG_BAD_ROW = 2
 

@@ -82,12 +82,13 @@ def quantized_matmul(x, w, scales, biases, transpose: bool = True, group_size: i
     return y
 
 
-def swiglu(gate, up, *, scalar: bool = False) -> torch.Tensor:
+def swiglu(gate, up, *, scalar: bool = False, table: bool = False) -> torch.Tensor:
     """MLX ``swiglu(gate, up)`` with the fused Up epilogue's rounding points
     (``models/flashnext/metal_runtime.py:278-287, 895-907``): every step rounded
     to the input dtype.  ``scalar`` selects the per-element device sequence of
-    the decode kernels instead of the four-at-a-time one of the grouped kernels
-    (bit-identical)."""
+    the decode kernels and ``table`` the grouped gate/up epilogue's sequence
+    with the sigmoid looked up in a table, instead of the four-at-a-time one
+    (all bit-identical)."""
     g = require_cuda(gate, "gate")
     u = require_cuda(up, "up")
     dt = act_dtype(g, "gate")
@@ -95,8 +96,8 @@ def swiglu(gate, up, *, scalar: bool = False) -> torch.Tensor:
         raise ValueError("gate and up must have the same shape and dtype")
     out = torch.empty_like(g)
     lib = _lib.load()
-    _lib.check(lib.mq_swiglu(ptr(g), ptr(u), ptr(out), g.numel(), dt,
-                             _lib.MQ_SWIGLU_SCALAR if scalar else 0, stream_handle()), lib)
+    flags = (_lib.MQ_SWIGLU_SCALAR if scalar else 0) | (_lib.MQ_SWIGLU_TABLE if table else 0)
+    _lib.check(lib.mq_swiglu(ptr(g), ptr(u), ptr(out), g.numel(), dt, flags, stream_handle()), lib)
     return out
 
 

@@ -66,6 +66,13 @@ def test_validation_errors_without_device():
     assert "experts" in _lib.last_error(lib)
     assert lib.mq_q4_dequant(None, None, None, None, 1, 32, 32, None) == _lib.MQ_ERR_INVALID
     assert lib.mq_q4_unpack(None, None, 0, None) == _lib.MQ_OK  # empty is a no-op
+    # mq_swiglu checks pointers and flags before any launch (the pointers are never read here).
+    dummy = ctypes.c_void_p(16)
+    both = _lib.MQ_SWIGLU_SCALAR | _lib.MQ_SWIGLU_TABLE
+    assert lib.mq_swiglu(dummy, dummy, dummy, 4, _lib.MQ_BF16, both, None) == _lib.MQ_ERR_INVALID
+    assert "exclude" in _lib.last_error(lib)
+    assert lib.mq_swiglu(dummy, dummy, dummy, 4, _lib.MQ_BF16, 4, None) == _lib.MQ_ERR_INVALID
+    assert "flags" in _lib.last_error(lib)
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -4,8 +4,9 @@ The reference requires the SwiGLU epilogue to equal the bf16 sequence for
 every one of the 65,536 bf16 gates at up = 0x3F9E and 0x3F80, and on its
 representative bits (``models/flashnext/tests/unit/test_swiglu_contract.py:21-31, 37-83``).
 Here the device sequences the kernels run -- per element (decode epilogue),
-four at a time (grouped epilogue), and the sigmoid alone (shared-expert gate)
--- are compared bit for bit with ``oracle.moe.swiglu`` / ``sigmoid_t`` over
+four at a time, four at a time with the sigmoid from the per-block table
+(grouped gate/up epilogue), and the sigmoid alone (shared-expert gate) -- are
+compared bit for bit with ``oracle.moe.swiglu`` / ``sigmoid_t`` over
 every gate pattern at those ups and a few more.  NaN outputs must be NaN (the
 sign and payload of a NaN are not fixed by IEEE arithmetic and are not
 compared).  The one-instruction bf16 rounding is checked against integer
@@ -52,15 +53,16 @@ def _assert_bits(got, want, what):
                            f"got {[hex(int(got[i])) for i in bad[:6]]} want {[hex(int(want[i])) for i in bad[:6]]}")
 
 
-@pytest.mark.parametrize("scalar", [False, True], ids=["four-at-a-time", "per-element"])
-def test_swiglu_all_gates_bit_exact(torch_mod, scalar):
-    say(f"case: swiglu all 65536 gates x {len(UPS)} ups scalar={scalar}")
+@pytest.mark.parametrize("seq", ["runs", "scalar", "table"], ids=["four-at-a-time", "per-element", "table"])
+def test_swiglu_all_gates_bit_exact(torch_mod, seq):
+    say(f"case: swiglu all 65536 gates x {len(UPS)} ups sequence={seq}")
     from flashnext_hip import ops
 
     gates = np.tile(ALL_GATES, len(UPS))
     ups = np.repeat(np.array(UPS, dtype=np.uint16), 65536)
-    got = from_dev_bf16(ops.swiglu(to_dev_bf16(gates), to_dev_bf16(ups), scalar=scalar))
-    _assert_bits(got, moe.swiglu(gates, ups), f"swiglu scalar={scalar}")
+    got = from_dev_bf16(ops.swiglu(to_dev_bf16(gates), to_dev_bf16(ups), scalar=seq == "scalar",
+                                   table=seq == "table"))
+    _assert_bits(got, moe.swiglu(gates, ups), f"swiglu sequence={seq}")
 
 
 def test_swiglu_reference_representative_bits(torch_mod):
@@ -69,9 +71,9 @@ def test_swiglu_reference_representative_bits(torch_mod):
 
     g = np.array([0x0000, 0x3F80, 0xBF80, 0x4120, 0xC120], dtype=np.uint16)
     u = np.array([0x3F80, 0x3FA0, 0x3F00, 0x4020, 0xC000], dtype=np.uint16)
-    for scalar in (False, True):
+    for scalar, table in ((False, False), (True, False), (False, True)):
         # a 5-element call covers one run of four plus a one-element tail
-        got = from_dev_bf16(ops.swiglu(to_dev_bf16(g), to_dev_bf16(u), scalar=scalar))
+        got = from_dev_bf16(ops.swiglu(to_dev_bf16(g), to_dev_bf16(u), scalar=scalar, table=table))
         assert got.tolist() == moe.swiglu(g, u).tolist()
 
 
