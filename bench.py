@@ -420,11 +420,12 @@ def stack_bench(torch, dev, runners, stream, steps: int = 128) -> dict:
 
 
 def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_steps: int = 2,
-                  pool_gb: float = 6.0, copy_engines: int = 4) -> dict:
+                  pool_gb: float = 6.0, copy_engines: int = 4, method: str = "gather") -> dict:
     """The 48-block stack decoded through a 6 GB LRU hot pool: per layer the
     router runs, its experts are assigned slots on the host (hits move to the
     LRU tail, misses evict the head), missed records are copied from pinned
-    host memory on a copy stream, and the expert kernels read the pool through
+    host memory on a copy stream (`method`: one gather kernel per layer, or one
+    hipMemcpyAsync per record over `copy_engines` streams), and the expert kernels read the pool through
     slot words.  One host synchronisation per layer (the route hand-off), as in
     the reference's pool pass.  Host images are the 512 records of layer 0,
     shared by every layer (same bytes per copy as distinct images)."""
@@ -459,6 +460,9 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
     gen.manual_seed(6)
     xs = torch.randn((warm_steps + steps, L, 1, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
     copy_streams = [torch.cuda.Stream() for _ in range(copy_engines)]
+    # Pinned staging for the route words, so that their upload queues behind
+    # the refill on the compute stream instead of waiting for it on the host.
+    routes_host = [torch.empty(dl.routes.shape, dtype=dl.routes.dtype, pin_memory=True) for dl in dls]
     torch.cuda.synchronize()
 
     def step(s):
@@ -467,8 +471,9 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
             dl.launch_router(handle)
             inds = dl.inds.cpu()  # the route hand-off (synchronises the stream)
             slots, misses = pool.assign(l, sorted(set(inds.reshape(-1).tolist())))
-            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copy_streams)
-            dl.routes.copy_(HipExpertPool.route_words(slots, inds).to(dev, non_blocking=False))
+            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copy_streams, method=method)
+            routes_host[l].copy_(HipExpertPool.route_words(slots, inds).view(dl.routes.shape))
+            dl.routes.copy_(routes_host[l], non_blocking=True)
             dl.launch_experts(handle)
 
     with torch.cuda.stream(stream):
@@ -503,7 +508,7 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
             dl.launch_router(handle)
             inds = dl.inds.cpu()
             slots, misses = pool.assign(l, sorted(set(inds.reshape(-1).tolist())))
-            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copy_streams)
+            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copy_streams, method=method)
             dl.routes.copy_(HipExpertPool.route_words(slots, inds).to(dev, non_blocking=False))
             dl.launch_experts(handle)
             torch.cuda.synchronize()
@@ -515,7 +520,10 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
     miss_bytes = misses * stride
     out = {"workload": f"{L} stacked MoE blocks through a {pool_gb:g} GB LRU hot pool ({pool.slots} slots), "
                        f"{steps} decode steps, fresh N(0,1) hidden per step and layer, misses copied from pinned "
-                       f"host memory on {copy_engines} copy streams",
+                       + ("host memory by one gather kernel per layer (PCIe reads of the mapped records)"
+                          if method == "gather" else
+                          f"host memory by one hipMemcpyAsync per record on {copy_engines} copy streams"),
+           "refill": method,
            "us_per_token": round(ms * 1000, 1), "wall_us_per_token": round(wall_ms * 1000 / steps, 1),
            "slots": pool.slots, "expert_lookups_per_token": round(lookups, 1),
            "misses_per_token": round(misses, 1), "hit_rate": round(1 - misses / lookups, 4),
@@ -660,8 +668,9 @@ def main() -> int:
         print(json.dumps({"verify": [verify_bench(torch, dev, runners, stream, t) for t in (4, 16)]}), flush=True)
         return 0
     if args.hotpool_only:
-        print(json.dumps({"stack_hot_pool": [hotpool_bench(torch, dev, layers, runners, stream, copy_engines=n)
-                                             for n in (1, 2, 4)]}), flush=True)
+        runs = [hotpool_bench(torch, dev, layers, runners, stream, method="gather")]
+        runs += [hotpool_bench(torch, dev, layers, runners, stream, copy_engines=n, method="memcpy") for n in (1, 4)]
+        print(json.dumps({"stack_hot_pool": runs}), flush=True)
         return 0
     log("capturing graphs")
     # Step i decodes one token through layer i mod L.  The timed K steps (and
@@ -722,7 +731,10 @@ def main() -> int:
         log(f"verify: {extras['verify']}")
         extras["stack"] = stack_bench(torch, dev, runners, stream)
         log(f"stack: {extras['stack']}")
-        extras["stack_hot_pool"] = hotpool_bench(torch, dev, layers, runners, stream)
+        extras["stack_hot_pool"] = hotpool_bench(torch, dev, layers, runners, stream, method="gather")
+        memcpy = hotpool_bench(torch, dev, layers, runners, stream, method="memcpy")
+        extras["stack_hot_pool"]["memcpy_refill"] = {k: memcpy[k] for k in ("workload", "us_per_token", "h2d_gbps",
+                                                                            "check")}
         log(f"stack hot pool: {extras['stack_hot_pool']}")
         extras["peaks_measured"] = peaks_bench(torch, dev)
         log(f"peaks: {extras['peaks_measured']}")

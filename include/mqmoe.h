@@ -344,6 +344,20 @@ int mq_pool_refill_async(uint8_t *pool, uint64_t pool_header, uint64_t pool_stri
                          uint32_t n, uint64_t record_bytes, void *copy_stream,
                          void *done_event);
 
+/* The same refill (same arguments, ordering and slot checks) as one gather
+ * kernel on copy_stream that reads the records through their device mapping
+ * (PCIe reads of pinned host memory) instead of one hipMemcpyAsync per
+ * record; up to 16 records per launch.  Each host_records[i] must be pinned
+ * and device-mapped (hipHostMalloc; checked with hipHostGetDevicePointer
+ * before any launch) and 16-byte aligned, and record_bytes, pool_header and
+ * pool_stride multiples of 16.  The records must stay allocated until
+ * done_event (or the stream) completes.  Replaces the same fill
+ * (models/flashnext/expert_pool.py:133-145) as mq_pool_refill_async. */
+int mq_pool_refill_gather_async(uint8_t *pool, uint64_t pool_header, uint64_t pool_stride, uint32_t pool_slots,
+                                const uint32_t *slots, const void *const *host_records,
+                                uint32_t n, uint64_t record_bytes, void *copy_stream,
+                                void *done_event);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,7 +36,7 @@ EXPORTS = (
     "mq_swiglu", "mq_sigmoid", "mq_bf16_round_check",
     "mq_route_topk", "mq_moe_decode", "mq_moe_layer", "mq_grouped_workspace_size",
     "mq_moe_grouped", "mq_moe_grouped_static", "mq_gather_qmm_workspace_size", "mq_gather_qmm",
-    "mq_pool_refill_async",
+    "mq_pool_refill_async", "mq_pool_refill_gather_async",
 )
 
 
@@ -197,6 +197,7 @@ def _declare(lib) -> None:
         "mq_gather_qmm_workspace_size": ([u32, u32], u64),
         "mq_gather_qmm": ([c.POINTER(MqGatherArgs), vp], i32),
         "mq_pool_refill_async": ([vp, u64, u64, u32, vp, vp, u32, u64, vp, vp], i32),
+        "mq_pool_refill_gather_async": ([vp, u64, u64, u32, vp, vp, u32, u64, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

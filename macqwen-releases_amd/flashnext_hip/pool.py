@@ -11,7 +11,9 @@ records (``fill`` ``:133-145``).
 The region is HBM (a device tensor), the decode and grouped kernels address
 its records in place through slot words (``0x80000000 | slot``), and a miss
 is one pinned host-to-device copy of the whole record image on a side stream
-(``mq_pool_refill_async``) instead of nine file reads.  Ordering follows the
+instead of nine file reads: by default one gather kernel per fill that reads
+the pinned records over PCIe (``mq_pool_refill_gather_async``), or one
+``hipMemcpyAsync`` per record (``mq_pool_refill_async``).  Ordering follows the
 reference's rule that a slot is only overwritten after its last reader
 finished: the copy stream first waits for everything already queued on the
 compute stream, and the compute stream then waits for the copies.
@@ -124,19 +126,30 @@ class HipExpertPool:
         return placed, to_fill
 
     # ------------------------------------------------------------ refill (expert_pool.py:112-145)
-    def fill(self, layer: int, misses, store: HostRecordStore, *, compute_stream=None, copy_stream=None):
+    def fill(self, layer: int, misses, store: HostRecordStore, *, compute_stream=None, copy_stream=None,
+             method: str = "gather"):
         """Copy the missed records from pinned host memory into their slots.
 
         The copies run on ``copy_stream`` after everything already queued on
         ``compute_stream`` (earlier readers of the victim slots); the compute
-        stream then waits for them.  ``copy_stream`` may also be a sequence of
-        streams: the misses are split into contiguous shares, one per stream,
-        so that several DMA engines move them at once.  Returns the completion
-        events (one per copy stream) as a list, or the single event.
+        stream then waits for them.  ``method="gather"`` moves all misses with
+        one kernel that reads the pinned records over PCIe
+        (``mq_pool_refill_gather_async``) on the first copy stream;
+        ``method="memcpy"`` issues one ``hipMemcpyAsync`` per record
+        (``mq_pool_refill_async``), and then ``copy_stream`` may be a sequence
+        of streams: the misses are split into contiguous shares, one per
+        stream, so that several DMA engines move them at once.  Returns the
+        completion events (one per copy stream used) as a list when
+        ``copy_stream`` is a sequence, else the single event.
         """
+        if method not in ("gather", "memcpy"):
+            raise ValueError(f"method must be 'gather' or 'memcpy', got {method!r}")
         compute = compute_stream if compute_stream is not None else torch.cuda.current_stream(self.buffer.device)
         copies = list(copy_stream) if isinstance(copy_stream, (list, tuple)) else \
             [copy_stream if copy_stream is not None else compute]
+        if method == "gather":
+            copies = copies[:1]
+        refill = self._lib.mq_pool_refill_gather_async if method == "gather" else self._lib.mq_pool_refill_async
         misses = list(misses)
         recs = [store.record(layer, e) for e, _slot in misses]  # owned by the store: outlive the copies
         share = -(-len(misses) // len(copies)) if misses else 0
@@ -150,9 +163,8 @@ class HipExpertPool:
             n = len(part)
             slots = (ctypes.c_uint32 * max(n, 1))(*[int(slot) for _e, slot in part])
             ptrs = (ctypes.c_void_p * max(n, 1))(*[r.data_ptr() for r in part_recs])
-            rc = self._lib.mq_pool_refill_async(
-                ctypes.c_void_p(self.buffer.data_ptr()), HEADER_SIZE, self.stride, self.slots, slots, ptrs, n,
-                self.stride, ctypes.c_void_p(copy.cuda_stream), None)
+            rc = refill(ctypes.c_void_p(self.buffer.data_ptr()), HEADER_SIZE, self.stride, self.slots, slots, ptrs, n,
+                        self.stride, ctypes.c_void_p(copy.cuda_stream), None)
             _lib.check(rc, self._lib)
             done.record(copy)
             events.append(done)

@@ -73,6 +73,23 @@ def test_validation_errors_without_device():
     assert "exclude" in _lib.last_error(lib)
     assert lib.mq_swiglu(dummy, dummy, dummy, 4, _lib.MQ_BF16, 4, None) == _lib.MQ_ERR_INVALID
     assert "flags" in _lib.last_error(lib)
+    # the gather refill checks its arguments before any HIP call
+    slots = (ctypes.c_uint32 * 1)(0)
+    recs = (ctypes.c_void_p * 1)(16)
+    assert lib.mq_pool_refill_gather_async(None, 4096, 1 << 20, 4, slots, recs, 1, 1 << 20, None, None) \
+        == _lib.MQ_ERR_INVALID
+    assert lib.mq_pool_refill_gather_async(dummy, 4096, 1 << 20, 4, slots, recs, 1, 1000, None, None) \
+        == _lib.MQ_ERR_INVALID
+    assert "16-byte" in _lib.last_error(lib)
+    recs[0] = 24  # unaligned record
+    assert lib.mq_pool_refill_gather_async(dummy, 4096, 1 << 20, 4, slots, recs, 1, 1 << 20, None, None) \
+        == _lib.MQ_ERR_INVALID
+    assert "aligned" in _lib.last_error(lib)
+    recs[0] = 32
+    slots[0] = 4  # outside the pool
+    assert lib.mq_pool_refill_gather_async(dummy, 4096, 1 << 20, 4, slots, recs, 1, 1 << 20, None, None) \
+        == _lib.MQ_ERR_INVALID
+    assert "outside" in _lib.last_error(lib)
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -202,10 +202,11 @@ def stack48(torch_mod):
     return layers, resident
 
 
-def _hot_pool_run(torch, layers, resident, pool_bytes, steps, seed):
+def _hot_pool_run(torch, layers, resident, pool_bytes, steps, seed, method="gather"):
     """Decode `steps` tokens through all layers twice: resident, and through an
-    LRU hot pool refilled from pinned host records.  Returns the pool and the
-    list of (step, layer, resident bits, hot bits)."""
+    LRU hot pool refilled from pinned host records (`method`: the gather kernel
+    or one hipMemcpyAsync per record).  Returns the pool and the list of
+    (step, layer, resident bits, hot bits)."""
     from flashnext_hip import _lib
     from flashnext_hip.layout import HEADER_SIZE
     from flashnext_hip.moe_block import DecodeLayer, LayerWeights
@@ -249,7 +250,7 @@ def _hot_pool_run(torch, layers, resident, pool_bytes, steps, seed):
             for e in experts:
                 record(l, e)
             slots, misses = pool.assign(l, experts)
-            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copy_streams)
+            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copy_streams, method=method)
             dl.routes.copy_(HipExpertPool.route_words(slots, inds).to("cuda"))
             dl.launch_experts(handle)
             torch.cuda.synchronize()
@@ -283,12 +284,12 @@ def test_stack48_hot_pool_bit_identical_to_resident(torch_mod, stack48):
 
 def test_stack48_small_pool_evictions_bit_identical(torch_mod, stack48):
     torch = torch_mod
-    say("case: 48-block stack through a 64-slot pool (evictions every step)")
+    say("case: 48-block stack through a 64-slot pool (evictions every step), one hipMemcpyAsync per record")
     from flashnext_hip.layout import make_layout
 
     layers, resident = stack48
     stride = make_layout(H, I, G).record_stride
-    pool, results = _hot_pool_run(torch, layers, resident, 4096 + 64 * stride, steps=1, seed=7600)
+    pool, results = _hot_pool_run(torch, layers, resident, 4096 + 64 * stride, steps=1, seed=7600, method="memcpy")
     assert pool.slots == 64
     assert pool.misses > 64  # the pool wrapped: later layers evicted earlier ones
     for s, l, a, b in results:

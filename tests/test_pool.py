@@ -100,14 +100,44 @@ def test_pool_refill_bytes_and_decode_through_slots():
     torch.cuda.synchronize()
     for e, slot in misses4:
         assert torch.equal(pool.record_bytes(slot).cpu(), store.record(4, e))
-    # misses split over two copy streams land in the same places
+    # one hipMemcpyAsync per record, split over two copy streams: the same bytes in the same places
     store.add_banks(5, banks)
     slots5, misses5 = pool.assign(5, [3, 8, 1, 10, 6])
-    events = pool.fill(5, misses5, store, copy_stream=[copy, torch.cuda.Stream()])
+    events = pool.fill(5, misses5, store, copy_stream=[copy, torch.cuda.Stream()], method="memcpy")
     assert isinstance(events, list) and len(events) == 2
     torch.cuda.synchronize()
     for e, slot in misses5:
         assert torch.equal(pool.record_bytes(slot).cpu(), store.record(5, e))
+    # the gather kernel (the default): one launch per fill on the first copy stream
+    store.add_banks(6, banks)
+    slots6, misses6 = pool.assign(6, list(range(12)))
+    events = pool.fill(6, misses6, store, copy_stream=[copy, torch.cuda.Stream()])
+    assert isinstance(events, list) and len(events) == 1
+    torch.cuda.synchronize()
+    for e, slot in misses6:
+        assert torch.equal(pool.record_bytes(slot).cpu(), store.record(6, e)), (e, slot)
+    # 17 records in one call: two launches (16 records per launch), slot 0 written by both, in stream order
+    lib = _lib.load()
+    import ctypes
+
+    recs = [store.record(6, e % 12) for e in range(17)]
+    slots17 = list(range(16)) + [0]
+    pool.buffer[HEADER_SIZE:HEADER_SIZE + 16 * pool.stride].zero_()
+    n = len(recs)
+    _lib.check(lib.mq_pool_refill_gather_async(
+        ctypes.c_void_p(pool.buffer.data_ptr()), HEADER_SIZE, pool.stride, pool.slots,
+        (ctypes.c_uint32 * n)(*slots17), (ctypes.c_void_p * n)(*[r.data_ptr() for r in recs]), n, pool.stride,
+        ctypes.c_void_p(copy.cuda_stream), None), lib)
+    torch.cuda.synchronize()
+    for i in range(1, 16):
+        assert torch.equal(pool.record_bytes(slots17[i]).cpu(), recs[i]), i
+    assert torch.equal(pool.record_bytes(0).cpu(), recs[16])
+    with pytest.raises(ValueError):  # pageable memory is refused before any launch
+        pageable = torch.zeros(pool.stride, dtype=torch.uint8)
+        _lib.check(lib.mq_pool_refill_gather_async(
+            ctypes.c_void_p(pool.buffer.data_ptr()), HEADER_SIZE, pool.stride, pool.slots,
+            (ctypes.c_uint32 * 1)(1), (ctypes.c_void_p * 1)(pageable.data_ptr()), 1, pool.stride,
+            ctypes.c_void_p(copy.cuda_stream), None), lib)
     with pytest.raises(ValueError):  # a slot outside the pool is rejected before any copy
         lib = _lib.load()
         import ctypes
