@@ -696,10 +696,11 @@ void launch_gateup_r(const MqMoeArgs &a, const SharedExpert &shared, bool has_sh
                      a.hidden, a.inter, a.group_size, a.expert_count, tiles, err);
 }
 
-// Gate/up launch.  With routes given and 64-lane slices, a wave takes 2, 4 or
-// 8 rows per tile: the smallest count whose grid is resident at once, so that
-// many-token calls (speculative verify) stream in one round of blocks rather
-// than in successive rounds that each pay the full memory latency.
+// Gate/up launch.  With 64-lane slices a wave takes 2, 4 or 8 rows per tile:
+// the smallest count whose grid is resident at once, so that many-token calls
+// (speculative verify) stream in one round of blocks rather than in
+// successive rounds that each pay the full memory latency (and, with the
+// selection folded in, the selection's latency).
 template <class TT, bool SELECT>
 int launch_gateup(const MqMoeArgs &a, const SharedExpert &shared, bool has_shared, const int32_t *keeps,
                   const SelectParams &sel, const SelectOutputs &sel_out, typename TT::storage *act,
@@ -707,14 +708,14 @@ int launch_gateup(const MqMoeArgs &a, const SharedExpert &shared, bool has_share
   const Geometry g = geometry(a.hidden);
   const uint32_t pairs = a.tokens * a.slots + (has_shared ? a.tokens : 0u);
   MQ_GEOM_SWITCH(g, {
-    if constexpr (SW == 64 && !SELECT) {
+    if constexpr (SW == 64) {
       const auto blocks = [&](uint32_t r) { return static_cast<int64_t>(ceil_div(pairs * ceil_div(a.inter, r), kWaves)); };
-      if (blocks(2) <= resident_blocks<gateup_ptr<TT, SW, CPL, 2, false>>()) {
-        launch_gateup_r<TT, SW, CPL, 2, false>(a, shared, has_shared, keeps, sel, sel_out, act, err, pairs, stream);
-      } else if (blocks(4) <= resident_blocks<gateup_ptr<TT, SW, CPL, 4, false>>()) {
-        launch_gateup_r<TT, SW, CPL, 4, false>(a, shared, has_shared, keeps, sel, sel_out, act, err, pairs, stream);
+      if (blocks(2) <= resident_blocks<gateup_ptr<TT, SW, CPL, 2, SELECT>>()) {
+        launch_gateup_r<TT, SW, CPL, 2, SELECT>(a, shared, has_shared, keeps, sel, sel_out, act, err, pairs, stream);
+      } else if (blocks(4) <= resident_blocks<gateup_ptr<TT, SW, CPL, 4, SELECT>>()) {
+        launch_gateup_r<TT, SW, CPL, 4, SELECT>(a, shared, has_shared, keeps, sel, sel_out, act, err, pairs, stream);
       } else {
-        launch_gateup_r<TT, SW, CPL, 8, false>(a, shared, has_shared, keeps, sel, sel_out, act, err, pairs, stream);
+        launch_gateup_r<TT, SW, CPL, 8, SELECT>(a, shared, has_shared, keeps, sel, sel_out, act, err, pairs, stream);
       }
     } else {
       constexpr int R = steps_for<SW>();
@@ -999,11 +1000,11 @@ extern "C" int mq_moe_layer(const MqRouteArgs *route, const MqMoeArgs *moe, void
   a.keeps = r.keeps;
   if ((rc = validate_moe_args(a, true))) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (r.tokens >= 2) {
-    // Several tokens: one selection pass, then the expert kernels with routes
-    // given.  Folding the selection into every gate/up block (as for one
-    // token) would make the larger grid run in several rounds of blocks,
-    // each repeating the selection's latency.
+  if (r.tokens > static_cast<uint32_t>(kWaves)) {
+    // More tokens than a block has waves: one selection pass, then the expert
+    // kernels with routes given.  Folded into every gate/up block (as for up
+    // to four tokens, one per wave, in parallel) the selection would take
+    // several rounds per block, and the larger grid several rounds of blocks.
     if ((rc = mq_route_topk(&r, stream))) return rc;
     if (r.threshold >= 1.0f) a.keeps = nullptr;
     return moe_decode_t<BF16T>(a, s, nullptr, nullptr);

@@ -73,7 +73,7 @@ def decode_layer_512(torch_mod):
     return lay, w
 
 
-@pytest.mark.parametrize("tokens", [1, 4, 16])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 5, 16])  # up to 4: selection folded into gate/up, one token per wave
 def test_decode_layer_512_experts_matches_oracle(torch_mod, decode_layer_512, tokens):
     torch = torch_mod
     say(f"case: 512-expert routed decode layer tokens={tokens}")

@@ -59,7 +59,8 @@ def layer(torch_mod):
     return weights, recs, perm, wg, wsg
 
 
-@pytest.mark.parametrize("tokens,threshold", [(1, 1.0), (5, 0.85), (8, 1.0), (9, 1.0), (40, 0.85), (130, 1.0)])
+@pytest.mark.parametrize("tokens,threshold", [(1, 1.0), (3, 0.85), (4, 1.0), (5, 0.85), (8, 1.0), (9, 1.0), (40, 0.85),
+                                              (130, 1.0)])
 def test_moe_block_matches_oracle_on_both_paths(torch_mod, layer, tokens, threshold):
     torch = torch_mod
     say(f"case: moe block tokens={tokens} threshold={threshold}")
@@ -153,24 +154,26 @@ def test_segmented_sorted_rows_equal_one_call(torch_mod):
     assert torch.equal(y_all.view(torch.int16), y_seg.view(torch.int16))
 
 
-def test_many_token_layer_rows_equal_single_token_layers(torch_mod, layer):
-    """Tokens are independent: a 16-token routed layer (one selection pass, the
-    expert kernels taking several row groups per wave, the router's token
-    groups) gives each token the bits of a 1-token layer (selection folded into
-    gate/up, one row group per wave)."""
+@pytest.mark.parametrize("tokens", [3, 16])
+def test_many_token_layer_rows_equal_single_token_layers(torch_mod, layer, tokens):
+    """Tokens are independent: a many-token routed layer (16 tokens: one
+    selection pass, the expert kernels taking several row groups per wave, the
+    router's token groups; 3 tokens: the selection folded into gate/up, one
+    token per wave) gives each token the bits of a 1-token layer (selection
+    folded into gate/up, one row group per wave)."""
     torch = torch_mod
-    say("case: 16-token layer rows vs 1-token layers")
+    say(f"case: {tokens}-token layer rows vs 1-token layers")
     from flashnext_hip.moe_block import DecodeLayer
 
     weights = layer[0]
     for threshold in (1.0, 0.85):
-        many = DecodeLayer(weights, 16, K, threshold=threshold, min_keep=2)
+        many = DecodeLayer(weights, tokens, K, threshold=threshold, min_keep=2)
         one = DecodeLayer(weights, 1, K, threshold=threshold, min_keep=2)
-        x = to_dev_bf16(bf16_normal((16, H), seed=540))
+        x = to_dev_bf16(bf16_normal((tokens, H), seed=540))
         many.x.copy_(x)
         many.launch(None)
         torch.cuda.synchronize()
-        for t in range(16):
+        for t in range(tokens):
             one.x.copy_(x[t:t + 1])
             one.launch(None)
             torch.cuda.synchronize()
