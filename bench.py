@@ -17,6 +17,7 @@ layer divided by the step time.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -534,6 +535,110 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
     return out
 
 
+def floors_bench(torch, dev, layers, stream, graph_launches: int = 48, replays: int = 20) -> dict:
+    """Latency floors of the decode layer on this GPU, each as microseconds per
+    launch over HIP graphs of `graph_launches` launches: an empty kernel; 704
+    blocks of 256 threads that read next to nothing (the expert kernels' grid); one
+    kernel streaming a layer's expert bytes (11 records of 1,966,080 B, no
+    compute) from random slots of the 48 layers' pools (a new set per launch,
+    so from HBM), from one contiguous region, and from the same 11 records
+    every launch (resident in the last-level cache); the gate/up share then
+    the down share of the 11 records as two kernels; and a pointer chase of
+    eight links 2 MB apart, each chain written by the kernel before it, whose
+    first link is the first dependent load after a kernel boundary."""
+    import numpy as np
+
+    from flashnext_hip import _lib
+    from flashnext_hip.layout import HEADER_SIZE
+
+    lib = _lib.load()
+    handle = stream.cuda_stream
+    lay0 = layers[0].layout
+    stride = lay0.record_stride
+    down_off = lay0.offset("down_proj", "weight")
+    G, N = graph_launches, TOP_K + 1
+    rng = np.random.default_rng(5)
+    L = len(layers)
+    assert all(lay.pool.numel() >= HEADER_SIZE + EXPERTS * stride for lay in layers)
+    bases = [lay.pool.data_ptr() + HEADER_SIZE for lay in layers]
+    rec = np.array([[bases[int(l)] + int(s) * stride for l, s in zip(rng.integers(0, L, N), rng.integers(0, EXPERTS, N))]
+                    for _ in range(G)], dtype=np.uint64)
+    contig = np.array([[bases[k % L] + (k // L) * N * stride] for k in range(G)], dtype=np.uint64)
+    assert all((k // L + 1) * N <= EXPERTS for k in range(G))  # the contiguous runs stay inside one pool
+    segs = torch.from_numpy(rec.view(np.int64)).to(dev)
+    segs_down = torch.from_numpy((rec + np.uint64(down_off)).view(np.int64)).to(dev)
+    segs_contig = torch.from_numpy(contig.view(np.int64)).to(dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    blocks = N * 64
+
+    def probe(seg_tensor, k, n, nbytes):
+        ptr = ctypes.c_void_p(seg_tensor.data_ptr() + 8 * n * k) if n else None
+        _lib.check(lib.mq_stream_probe(ptr, n, nbytes, blocks if n else 1, ctypes.c_void_p(sink.data_ptr()), handle), lib)
+
+    cases = {
+        "empty_kernel": lambda: [probe(segs, k, 0, 0) for k in range(G)],
+        "dispatch_704_blocks": lambda: [probe(segs, k, N, 16) for k in range(G)],
+        "layer_bytes_random_records": lambda: [probe(segs, k, N, stride) for k in range(G)],
+        "layer_bytes_contiguous": lambda: [_lib.check(lib.mq_stream_probe(
+            ctypes.c_void_p(segs_contig.data_ptr() + 8 * k), 1, N * stride, blocks, ctypes.c_void_p(sink.data_ptr()),
+            handle), lib) for k in range(G)],
+        "layer_bytes_cache_resident": lambda: [probe(segs, 0, N, stride) for _ in range(G)],
+        "gateup_then_down_two_kernels": lambda: [(probe(segs, k, N, down_off), probe(segs_down, k, N, stride - down_off))
+                                                 for k in range(G)],
+    }
+    out = {"workload": f"HIP graphs of {G} launches; 11 records = {N * stride} B per launch",
+           "record_bytes": stride}
+    with torch.cuda.stream(stream):
+        for name, fn in cases.items():
+            fn()  # eager run (also checks the arguments)
+            torch.cuda.synchronize()
+            g = capture(torch, fn, stream)
+            time_graph(torch, g, 2, stream)
+            us = time_graph(torch, g, replays, stream) * 1000 / (replays * G)
+            row = {"us_per_launch": round(us, 3)}
+            if name.startswith("layer_bytes"):
+                row["tbps"] = round(N * stride / (us * 1e-6) / 1e12, 2)
+            out[name] = row
+            del g
+        # Pointer chase: chain k has 8 links 2 MB apart in its own 16 MB region.
+        hops, span = 8, 2 << 20
+        buf = torch.zeros(G * hops * span // 8, dtype=torch.int64, device=dev)
+        base = buf.data_ptr()
+        here = np.arange(G * hops, dtype=np.int64) * span
+        last = (np.arange(G * hops) % hops) == hops - 1
+        nxt = np.where(last, here, here + span)  # the last value is read, never followed
+        assert int(nxt.max()) + 8 <= buf.numel() * 8
+        idx = torch.from_numpy(here // 8).to(dev).view(G, hops)
+        vals = torch.from_numpy(base + nxt).to(dev).view(G, hops)
+        stamps = torch.zeros((G, 10), dtype=torch.int64, device=dev)
+        torch.cuda.synchronize()
+        chains = {}
+        for reader in (0, 1, 5):  # the block of the reading thread: XCD 0 (the writer's, one block), 1, 5
+
+            def chase():  # each chain is written by one kernel and followed by the next, as route words are
+                for k in range(G):
+                    buf.index_put_((idx[k],), vals[k])
+                    _lib.check(lib.mq_hop_probe(ctypes.c_void_p(base + k * hops * span), hops,
+                                                ctypes.c_void_p(stamps[k].data_ptr()), reader, handle), lib)
+            chase()
+            torch.cuda.synchronize()
+            g = capture(torch, chase, stream)
+            for _ in range(3):
+                g.replay()
+            torch.cuda.synchronize()
+            st = stamps.cpu().numpy()
+            d = np.diff(st[:, :hops + 1], axis=1) * 0.01  # 100 MHz ticks -> us
+            chains[f"reader_block_{reader}"] = {"first_link_us_median": round(float(np.median(d[:, 0])), 3),
+                                                "later_links_us_median": round(float(np.median(d[:, 1:])), 3)}
+            del g
+        chains["note"] = ("one thread, links 2 MB apart in device memory, each chain written by a one-block "
+                          "index_put_ kernel just before and followed right after the kernel boundary by a thread "
+                          "of the given block (blocks go to XCDs round-robin); 100 MHz real-time clock")
+        out["dependent_load_chain"] = chains
+        del buf
+    return out
+
+
 def peaks_bench(torch, dev) -> dict:
     """Measured ceilings on this GPU: a 1 GiB device copy and a bf16 GEMM."""
     a = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -624,6 +729,7 @@ def main() -> int:
     ap.add_argument("--prefill-only", action="store_true", help="time only the 4096-token prefill grouped path")
     ap.add_argument("--verify-only", action="store_true", help="time only the 4- and 16-token verify layers")
     ap.add_argument("--hotpool-only", action="store_true", help="time only the 6 GB hot-pool stack")
+    ap.add_argument("--floors-only", action="store_true", help="time only the decode latency floors")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the expert-parallel "
@@ -666,6 +772,9 @@ def main() -> int:
         return 0
     if args.verify_only:
         print(json.dumps({"verify": [verify_bench(torch, dev, runners, stream, t) for t in (4, 16)]}), flush=True)
+        return 0
+    if args.floors_only:
+        print(json.dumps({"floors": floors_bench(torch, dev, layers, stream)}), flush=True)
         return 0
     if args.hotpool_only:
         runs = [hotpool_bench(torch, dev, layers, runners, stream, method="gather")]
@@ -736,6 +845,8 @@ def main() -> int:
         extras["stack_hot_pool"]["memcpy_refill"] = {k: memcpy[k] for k in ("workload", "us_per_token", "h2d_gbps",
                                                                             "check")}
         log(f"stack hot pool: {extras['stack_hot_pool']}")
+        extras["floors"] = floors_bench(torch, dev, layers, stream)
+        log(f"floors: {extras['floors']}")
         extras["peaks_measured"] = peaks_bench(torch, dev)
         log(f"peaks: {extras['peaks_measured']}")
     prefill = None

@@ -257,6 +257,27 @@ int mq_sigmoid(const void *x, void *out, uint64_t n, int dtype, void *stream);
  * counterpart: it exists so the exactness claim is tested on each device. */
 int mq_bf16_round_check(uint64_t first, uint64_t count, unsigned long long *counts, void *stream);
 
+/* ---- latency floors of the decode path (measurement only) ----
+ * No reference counterpart: they measure, on the device at hand, what a
+ * kernel boundary, a stream of expert bytes with no compute, and a dependent
+ * load cost, which bound the decode layer from below (bench.py --floors).
+ *
+ * mq_stream_probe: one kernel reading n segments of bytes_each bytes (a
+ * multiple of 16) at the device addresses segments[0..n) (a DEVICE array)
+ * with non-temporal 16-byte loads, `blocks` blocks (a multiple of n) of 256
+ * threads splitting them; `sink` is a device word written only on a
+ * checksum match.  n = 0 launches an empty kernel.
+ * mq_hop_probe: thread 0 of block `block` (0..63; blocks are dealt to the
+ * XCDs round-robin, so the block picks the XCD) follows `hops` (1..8) links of
+ * a pointer chain in device memory starting at `chain` (each link holds the
+ * device address of the next; the caller makes every dereferenced link
+ * valid) and writes 10 words to `stamps`: the 100 MHz real-time clock at the
+ * start and after each link (unused entries repeat the last), then the final
+ * value read. */
+int mq_stream_probe(const uint64_t *segments, uint32_t n, uint64_t bytes_each, uint32_t blocks, uint32_t *sink,
+                    void *stream);
+int mq_hop_probe(const uint64_t *chain, uint32_t hops, uint64_t *stamps, uint32_t block, void *stream);
+
 /* ---- router ---- */
 int mq_route_topk(const MqRouteArgs *args, void *stream);
 

@@ -90,6 +90,14 @@ def test_validation_errors_without_device():
     assert lib.mq_pool_refill_gather_async(dummy, 4096, 1 << 20, 4, slots, recs, 1, 1 << 20, None, None) \
         == _lib.MQ_ERR_INVALID
     assert "outside" in _lib.last_error(lib)
+    # the latency probes check their arguments before any launch
+    assert lib.mq_stream_probe(None, 11, 1 << 20, 704, dummy, None) == _lib.MQ_ERR_INVALID
+    assert lib.mq_stream_probe(dummy, 11, 1000, 704, dummy, None) == _lib.MQ_ERR_INVALID
+    assert lib.mq_stream_probe(dummy, 11, 1 << 20, 700, dummy, None) == _lib.MQ_ERR_INVALID
+    assert lib.mq_hop_probe(dummy, 0, dummy, 0, None) == _lib.MQ_ERR_INVALID
+    assert lib.mq_hop_probe(dummy, 9, dummy, 0, None) == _lib.MQ_ERR_INVALID
+    assert lib.mq_hop_probe(None, 4, dummy, 0, None) == _lib.MQ_ERR_INVALID
+    assert lib.mq_hop_probe(dummy, 4, dummy, 64, None) == _lib.MQ_ERR_INVALID
 
 
 def test_missing_library_fails_loudly(tmp_path):
