@@ -285,11 +285,12 @@ int mq_route_topk(const MqRouteArgs *args, void *stream);
 int mq_moe_decode(const MqMoeArgs *args, void *stream);
 
 /* One routed decode layer, _moe_call with the fused executor
- * (models/flashnext/adaptive_topk.py:53-292).  One token: router logits,
- * then a gate/up kernel that performs the top-k selection itself (writing
- * route->inds, scores (bf16), routes, keeps, shared_gate) and runs
- * gate/up/SwiGLU, then down + combine.  2..64 tokens: mq_route_topk, then the
- * expert kernels with the routes given (same outputs).  route->x must equal
+ * (models/flashnext/adaptive_topk.py:53-292).  Up to 4 tokens: router
+ * logits, then a gate/up kernel that performs the top-k selection itself (one
+ * token per wave of each block; writing route->inds, scores (bf16), routes,
+ * keeps, shared_gate) and runs gate/up/SwiGLU, then down + combine.
+ * 5..64 tokens: mq_route_topk, then the expert kernels with the routes given
+ * (same outputs).  route->x must equal
  * moe->x (bf16); route->logits_out and route->routes are required;
  * moe->routes/scores/keeps/shared_gate are taken from the route outputs.
  * No MQ_DECODE flags. */
