@@ -112,6 +112,12 @@ typedef struct MqMoeArgs {
 
 #define MQ_DECODE_RETURN_ALL 1u    /* write gate_out/up_out/act_out/down_out, skip combine */
 #define MQ_DECODE_UNFUSED_UP 2u    /* separate up projection + SwiGLU pass (bit-identical) */
+/* Combine in the reference's generic order at any group size: every score
+ * product rounded to T, the kept slots summed in float32 in slot order and
+ * rounded once, then the shared term (weighted_combine, metal_runtime.py:908-929;
+ * the order of _moe_call's gather_qmm path beyond the fused executor's token
+ * bound, adaptive_topk.py:274-277).  Group 64 always combines this way. */
+#define MQ_DECODE_GENERIC_COMBINE 4u
 
 /* Arguments of mq_route_topk: the router chain of _moe_call
  * (models/flashnext/adaptive_topk.py:53-64, 75-261; compiled.py:61-71) and
@@ -290,10 +296,9 @@ int mq_moe_decode(const MqMoeArgs *args, void *stream);
  * token per wave of each block; writing route->inds, scores (bf16), routes,
  * keeps, shared_gate) and runs gate/up/SwiGLU, then down + combine.
  * 5..64 tokens: mq_route_topk, then the expert kernels with the routes given
- * (same outputs).  route->x must equal
- * moe->x (bf16); route->logits_out and route->routes are required;
- * moe->routes/scores/keeps/shared_gate are taken from the route outputs.
- * No MQ_DECODE flags. */
+ * (same outputs).  route->x must equal moe->x (bf16); route->logits_out and
+ * route->routes are required; moe->routes/scores/keeps/shared_gate are taken
+ * from the route outputs.  moe->flags: 0 or MQ_DECODE_GENERIC_COMBINE. */
 int mq_moe_layer(const MqRouteArgs *route, const MqMoeArgs *moe, void *stream);
 
 /* ---- prefill / verify grouped path ---- */

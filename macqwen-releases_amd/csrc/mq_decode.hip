@@ -734,7 +734,7 @@ void launch_down_r(const MqMoeArgs &a, const SharedExpert &shared, int shared_mo
   hipLaunchKernelGGL((down_combine_kernel<TT, SW, CPL, SPW, R>), grid, dim3(kThreads), 0, stream, act, a.down, shared,
                      a.routes, a.scores, a.score_dtype, keeps, shared_mode, shared_vec, a.shared_gate,
                      static_cast<S *>(a.out), a.tokens, a.slots, a.hidden, a.inter, a.group_size, a.expert_count,
-                     a.group_size == 64, err);
+                     a.group_size == 64 || (a.flags & MQ_DECODE_GENERIC_COMBINE) != 0, err);
 }
 
 template <class TT, int SW, int CPL, int SPW, int R>
@@ -949,10 +949,12 @@ int validate_moe_args(const MqMoeArgs &a, bool routed_layer) {
     if (!routed_layer && a.scores == nullptr) return fail(MQ_ERR_INVALID, "scores are required unless return_all is set");
     if (a.out == nullptr) return fail(MQ_ERR_INVALID, "out is required");
     if (a.score_dtype != MQ_F32 && a.score_dtype != MQ_BF16) return fail(MQ_ERR_INVALID, "bad score dtype");
-    if (a.group_size == 64 && a.x_dtype == MQ_BF16 && a.score_dtype == MQ_F32)
+    if ((a.group_size == 64 || (a.flags & MQ_DECODE_GENERIC_COMBINE)) && a.x_dtype == MQ_BF16 &&
+        a.score_dtype == MQ_F32)
       return fail(MQ_ERR_UNSUPPORTED,
-                  "group 64 combines in the score dtype, so bf16 activations with float32 scores give a float32 "
-                  "result: use MQ_DECODE_RETURN_ALL and combine on the caller's side");
+                  "the generic combine (group 64, or MQ_DECODE_GENERIC_COMBINE) is in the score dtype, so bf16 "
+                  "activations with float32 scores give a float32 result: use MQ_DECODE_RETURN_ALL and combine on "
+                  "the caller's side");
     const int modes = (a.shared_y != nullptr) + (a.shared != nullptr) + (a.shared_expert != nullptr);
     if (modes > 1) return fail(MQ_ERR_INVALID, "provide shared_y, shared parts or a shared expert, not several");
     if ((a.shared != nullptr || a.shared_expert != nullptr) && a.shared_gate == nullptr)
@@ -990,7 +992,8 @@ extern "C" int mq_moe_layer(const MqRouteArgs *route, const MqMoeArgs *moe, void
   if (moe->x_dtype != MQ_BF16 || moe->x != r.x) return fail(MQ_ERR_INVALID, "the routed layer needs the same bf16 x");
   if (r.tokens != moe->tokens || r.top_k != moe->slots || r.hidden != moe->hidden)
     return fail(MQ_ERR_INVALID, "route and moe shapes disagree");
-  if (moe->flags != 0) return fail(MQ_ERR_INVALID, "the routed layer supports no MQ_DECODE flags");
+  if (moe->flags & ~MQ_DECODE_GENERIC_COMBINE)
+    return fail(MQ_ERR_INVALID, "the routed layer supports no MQ_DECODE flag but MQ_DECODE_GENERIC_COMBINE");
   if ((moe->shared_expert != nullptr) != (r.shared_gate != nullptr))
     return fail(MQ_ERR_INVALID, "a shared expert needs the router's shared_gate output and vice versa");
   a.routes = r.routes;

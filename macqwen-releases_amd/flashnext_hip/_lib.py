@@ -23,6 +23,7 @@ MQ_BF16 = 1
 MQ_SLOT_BIT = 0x80000000
 MQ_DECODE_RETURN_ALL = 1
 MQ_DECODE_UNFUSED_UP = 2
+MQ_DECODE_GENERIC_COMBINE = 4
 MQ_SWIGLU_SCALAR = 1
 MQ_SWIGLU_TABLE = 2
 MQ_DEVFLAG_BAD_ROUTE = 1

@@ -48,9 +48,13 @@ class DecodeLayer:
     """One MoE decode layer for a fixed token count, with preallocated buffers."""
 
     def __init__(self, weights: LayerWeights, tokens: int, top_k: int, *, threshold: float = 1.0,
-                 min_keep: int = 1, blend: float = 1.0, device="cuda", x: torch.Tensor | None = None):
+                 min_keep: int = 1, blend: float = 1.0, device="cuda", x: torch.Tensor | None = None,
+                 generic_combine: bool = False):
         """``x``: optional caller-owned bf16 ``[tokens, hidden]`` input buffer
-        (e.g. a row of a larger staging tensor); allocated here when omitted."""
+        (e.g. a row of a larger staging tensor); allocated here when omitted.
+        ``generic_combine``: combine the slots in the reference's generic bf16
+        order (every score product rounded to bf16, ``MQ_DECODE_GENERIC_COMBINE``)
+        instead of the fused executor's float32 order."""
         lay = weights.layout
         self.w = weights
         self.tokens, self.top_k = tokens, top_k
@@ -102,6 +106,7 @@ class DecodeLayer:
         a.out, a.act_out = ptr(self.out), ptr(self.act)
         a.tokens, a.slots, a.hidden, a.inter = tokens, top_k, self.hidden, self.inter
         a.expert_count, a.group_size = self.experts, lay.group_size
+        a.flags = _lib.MQ_DECODE_GENERIC_COMBINE if generic_combine else 0
         self.moe_args = a
         self._lib = _lib.load()
 
@@ -131,24 +136,31 @@ class MoEBlock:
     hands the scores to the fused executor, ``adaptive_topk.py:266-269``) the
     block runs a :class:`DecodeLayer` per token count: router, experts and the
     ordered float32 combine with ``shared_y`` in the down kernel.  Beyond it
-    the router runs on its own and the (token, slot) rows go through the
-    grouped path (``switch_mlp(x, inds)``), combined in bf16 as
-    ``(y * scores).sum(-2) + shared_gate * shared`` (``adaptive_topk.py:274-277``).
+    the reference sends the (token, slot) rows through ``switch_mlp(x, inds)``
+    and combines them in bf16 as ``(y * scores).sum(-2) + shared_gate * shared``
+    (``adaptive_topk.py:274-277``).  Here that is the routed decode layer
+    again, with the generic bf16 combine (``MQ_DECODE_GENERIC_COMBINE``), up
+    to ``routed_max_tokens`` tokens (64; at verify sizes it is 1.1-1.8x
+    faster than the grouped GEMMs, whose tiles hold one or two rows per expert
+    there), and the grouped path (sort + MFMA GEMMs + bf16 combine) beyond.
     At a keep threshold below 1 the dropped slots carry the row's first expert
-    and score 0 on both paths (``adaptive_topk.py:213-227``).
+    and score 0 on every path (``adaptive_topk.py:213-227``).
 
-    ``last_path`` is ``"fused"`` or ``"grouped"`` after each call.
+    ``last_path`` is ``"fused"``, ``"routed"`` or ``"grouped"`` after each call.
     """
 
     def __init__(self, weights: LayerWeights, top_k: int, *, threshold: float = 1.0, min_keep: int = 1,
-                 blend: float = 1.0, fused_max_tokens: int = 8):
+                 blend: float = 1.0, fused_max_tokens: int = 8, routed_max_tokens: int = 64):
         from .grouped import GroupedMoE
 
         if not 0 <= fused_max_tokens <= 8:
             raise ValueError("fused_max_tokens must be in 0..8")
+        if not (routed_max_tokens == 0 or fused_max_tokens <= routed_max_tokens <= 64):
+            raise ValueError("routed_max_tokens must be 0 or in fused_max_tokens..64")
         self.w = weights
         self.top_k, self.threshold, self.min_keep, self.blend = int(top_k), float(threshold), int(min_keep), float(blend)
         self.fused_max_tokens = int(fused_max_tokens)
+        self.routed_max_tokens = int(routed_max_tokens)
         self.device = weights.pool.device
         self.hidden, self.inter = weights.layout.hidden, weights.layout.inter
         self._layers: dict[int, DecodeLayer] = {}
@@ -174,15 +186,16 @@ class MoEBlock:
         if tokens == 0:
             raise ValueError("x has no tokens")
         stream = torch.cuda.current_stream(self.device).cuda_stream
-        if tokens <= self.fused_max_tokens:
+        fused = tokens <= self.fused_max_tokens
+        if fused or tokens <= self.routed_max_tokens:
             layer = self._layers.get(tokens)
             if layer is None:
                 layer = DecodeLayer(self.w, tokens, self.top_k, threshold=self.threshold, min_keep=self.min_keep,
-                                    blend=self.blend, device=self.device)
+                                    blend=self.blend, device=self.device, generic_combine=not fused)
                 self._layers[tokens] = layer
             layer.x.copy_(x)
             layer.launch(stream)
-            self.last_path = "fused"
+            self.last_path = "fused" if fused else "routed"
             self.last_route = layer
             return layer.out.clone()
         r = route(x, self.w.router_w, self.top_k, threshold=self.threshold, min_keep=self.min_keep,

@@ -59,30 +59,43 @@ def layer(torch_mod):
     return weights, recs, perm, wg, wsg
 
 
-@pytest.mark.parametrize("tokens,threshold", [(1, 1.0), (3, 0.85), (4, 1.0), (5, 0.85), (8, 1.0), (9, 1.0), (40, 0.85),
-                                              (130, 1.0)])
-def test_moe_block_matches_oracle_on_both_paths(torch_mod, layer, tokens, threshold):
+@pytest.mark.parametrize("tokens,threshold,routed_max", [
+    (1, 1.0, 64), (3, 0.85, 64), (4, 1.0, 64), (5, 0.85, 64), (8, 1.0, 64), (9, 1.0, 64), (40, 0.85, 64),
+    (64, 1.0, 64), (9, 1.0, 0), (40, 0.85, 0), (130, 1.0, 64)])
+def test_moe_block_matches_oracle_on_every_path(torch_mod, layer, tokens, threshold, routed_max):
     torch = torch_mod
-    say(f"case: moe block tokens={tokens} threshold={threshold}")
+    say(f"case: moe block tokens={tokens} threshold={threshold} routed_max={routed_max}")
     from flashnext_hip import _lib
     from flashnext_hip.moe_block import MoEBlock
 
     weights, recs, perm, wg, wsg = layer
-    block = MoEBlock(weights, K, threshold=threshold, min_keep=2)
+    block = MoEBlock(weights, K, threshold=threshold, min_keep=2, routed_max_tokens=routed_max)
     x = bf16_normal((tokens, H), seed=510 + tokens)
     out = block(to_dev_bf16(x))
     torch.cuda.synchronize()
     assert _lib.check_device_errors() == 0
-    assert block.last_path == ("fused" if tokens <= 8 else "grouped")
+    path = "fused" if tokens <= 8 else "routed" if tokens <= routed_max else "grouped"
+    assert block.last_path == path
     ref = orouter.route(x, wg, K, threshold=threshold, min_keep=2, slot_table=perm.astype(np.uint32))
     r = block.last_route
     assert np.array_equal(r.routes.cpu().numpy().view(np.uint32), ref["routes"])
     assert np.array_equal(from_dev_bf16(r.scores), ref["scores"])
     got = bf16.bf16_to_f32(from_dev_bf16(out))
-    if tokens <= 8:
+    keeps = ref["keeps"] if threshold < 1 else None
+    if path == "fused":
         want = moe.decode_layer(x, ref["inds"], ref["scores"], recs, score_dtype="bf16", shared_gate_weight=wsg,
-                                keeps=ref["keeps"] if threshold < 1 else None)
+                                keeps=keeps)
         assert_close(got, bf16.bf16_to_f32(want), f"fused block T={tokens}")
+        return
+    if path == "routed":  # the grouped path's semantics (generic bf16 combine) through the decode kernels
+        want = moe.decode_layer(x, ref["inds"], ref["scores"], recs, score_dtype="bf16", shared_gate_weight=wsg,
+                                keeps=keeps, combine="generic")
+        assert_close(got, bf16.bf16_to_f32(want), f"routed block T={tokens}")
+        width = ref["width"]
+        exact, _ = moe.prefill_layer(x, ref["inds"][:, :width], ref["scores"][:, :width], recs,
+                                     shared_gate_weight=wsg)
+        rep = value_report(got, bf16.bf16_to_f32(exact))
+        assert rep["cosine"] >= MIN_COSINE and rep["max_rel"] <= MAX_REL, rep
         return
     width = ref["width"]
     tiles, _ = moe.prefill_layer(x, ref["inds"][:, :width], ref["scores"][:, :width], recs,
@@ -244,9 +257,10 @@ def checkpoint_shape_layers(torch_mod):
 def test_moe_block_checkpoint_shape_adaptive_keep(torch_mod, checkpoint_shape_layers, group, tokens):
     """``_moe_call`` at the checkpoint shape (hidden 2560, inter 640: the
     non-fast 640-wide down path) with the chat default keep threshold 0.85
-    (``adaptive_topk.py:75-232``) on both paths: the routed layer up to 8
-    tokens (fused float32 combine at group 32, the generic bf16 order at group
-    64, ``metal_runtime.py:908-929``) and the grouped path beyond."""
+    (``adaptive_topk.py:75-232``) on every path: the fused routed layer up to
+    8 tokens (fused float32 combine at group 32, the generic bf16 order at group
+    64, ``metal_runtime.py:908-929``), beyond it the routed layer with the
+    generic bf16 combine and, with that path off, the grouped path."""
     torch = torch_mod
     say(f"case: moe block 2560/640 g{group} tokens={tokens} threshold=0.85")
     from flashnext_hip import _lib
@@ -272,11 +286,19 @@ def test_moe_block_checkpoint_shape_adaptive_keep(torch_mod, checkpoint_shape_la
                                 keeps=ref["keeps"], combine="generic" if group == 64 else "fused")
         assert_close(got, bf16.bf16_to_f32(want), f"fused block g{group} T={tokens}")
         return
-    assert block.last_path == "grouped"
+    assert block.last_path == "routed"
+    want = moe.decode_layer(x, ref["inds"], ref["scores"], recs, score_dtype="bf16", shared_gate_weight=wsg,
+                            keeps=ref["keeps"], combine="generic")
+    assert_close(got, bf16.bf16_to_f32(want), f"routed block g{group} T={tokens}")
+    # the grouped path at the same size (routed path off)
+    grouped = MoEBlock(weights, K, threshold=0.85, min_keep=2, routed_max_tokens=0)
+    got_g = bf16.bf16_to_f32(from_dev_bf16(grouped(to_dev_bf16(x))))
+    torch.cuda.synchronize()
+    assert grouped.last_path == "grouped"
     width = ref["width"]
     tiles, _ = moe.prefill_layer(x, ref["inds"][:, :width], ref["scores"][:, :width], recs,
                                  shared_gate_weight=wsg, weights="bf16")
-    assert_close(got, bf16.bf16_to_f32(tiles), f"grouped block g{group} T={tokens} (bf16 tiles)")
+    assert_close(got_g, bf16.bf16_to_f32(tiles), f"grouped block g{group} T={tokens} (bf16 tiles)")
 
 
 def test_group64_executor_shared_expert_generic_order(torch_mod, checkpoint_shape_layers):

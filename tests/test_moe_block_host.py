@@ -16,6 +16,11 @@ def test_moe_block_validates_arguments_before_device_work():
                      None, None)
     with pytest.raises(ValueError):
         MoEBlock(w, 2, fused_max_tokens=9)
+    with pytest.raises(ValueError):
+        MoEBlock(w, 2, routed_max_tokens=65)
+    with pytest.raises(ValueError):
+        MoEBlock(w, 2, fused_max_tokens=8, routed_max_tokens=5)
+    assert MoEBlock(w, 2, routed_max_tokens=0).routed_max_tokens == 0
     block = MoEBlock(w, 2)
     with pytest.raises(ValueError):
         block(torch.zeros((3, 128), dtype=torch.bfloat16))   # wrong width
