@@ -678,10 +678,26 @@ def peaks_bench(torch, dev) -> dict:
     end.record()
     torch.cuda.synchronize()
     tflops = 2 * n ** 3 * 20 / (start.elapsed_time(end) * 1e-3) / 1e12
+    del m1, m2
+    # Sustained issue rate of the grouped GEMMs' MFMA (v_mfma_f32_32x32x16_bf16,
+    # two waves per SIMD, register operands): the practical matrix ceiling.
+    from flashnext_hip import _lib
+    lib = _lib.load()
+    blocks, iters = 256, 20000
+    sink = torch.empty(blocks * 512, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.mq_mfma_probe(200, blocks, sink.data_ptr(), stream), lib)
+    torch.cuda.synchronize()
+    start.record()
+    _lib.check(lib.mq_mfma_probe(iters, blocks, sink.data_ptr(), stream), lib)
+    end.record()
+    torch.cuda.synchronize()
+    mfma_tflops = 2.0 * 32 * 32 * 16 * 4 * iters * 8 * blocks / (start.elapsed_time(end) * 1e-3) / 1e12
     return {"copy_gbps": round(copy_gbps, 1), "h2d_pinned_gbps": round(h2d_gbps, 1),
-            "bf16_gemm_tflops_8192": round(tflops, 1),
+            "bf16_gemm_tflops_8192": round(tflops, 1), "bf16_mfma_issue_tflops": round(mfma_tflops, 1),
             "note": "device-to-device copy counts read + write bytes; host-to-device from 256 MiB of pinned "
-                    "memory; GEMM through torch.matmul (hipBLASLt)"}
+                    "memory; GEMM through torch.matmul (hipBLASLt); MFMA issue rate from mq_mfma_probe "
+                    "(256 blocks x 8 waves x 80,000 independent v_mfma_f32_32x32x16_bf16 each)"}
 
 
 def load_traffic(kernel_tag: str):

@@ -283,6 +283,14 @@ int mq_bf16_round_check(uint64_t first, uint64_t count, unsigned long long *coun
 int mq_stream_probe(const uint64_t *segments, uint32_t n, uint64_t bytes_each, uint32_t blocks, uint32_t *sink,
                     void *stream);
 int mq_hop_probe(const uint64_t *chain, uint32_t hops, uint64_t *stamps, uint32_t block, void *stream);
+/* mq_mfma_probe: `blocks` blocks of 512 threads (two waves per SIMD at one
+ * block per CU), each wave issuing `iters` (1..2^24) rounds of four
+ * independent v_mfma_f32_32x32x16_bf16 (32,768 FLOP each) on register
+ * operands; `sink` is a device array of blocks * 512 floats.  Timing the
+ * launch gives the sustained bf16 MFMA rate at the clock the matrix cores
+ * hold under load, the practical ceiling of the grouped GEMMs.  No reference
+ * counterpart. */
+int mq_mfma_probe(uint32_t iters, uint32_t blocks, float *sink, void *stream);
 
 /* ---- router ---- */
 int mq_route_topk(const MqRouteArgs *args, void *stream);

@@ -1,8 +1,9 @@
-// Memory-latency floors of the decode design, measured on the device the
-// library runs on: the cost of a kernel boundary, of streaming a layer's
-// expert bytes with no compute, and of a dependent load right after a kernel
-// starts.  The decode layer is a chain of such boundaries and hops, so these
-// figures bound it from below.  No reference counterpart.
+// Floors measured on the device the library runs on: the cost of a kernel
+// boundary, of streaming a layer's expert bytes with no compute, and of a
+// dependent load right after a kernel starts (the decode layer is a chain of
+// such boundaries and hops, so these bound it from below), and the sustained
+// issue rate of the bf16 MFMA the grouped GEMMs use.  No reference
+// counterpart.
 #include <hip/hip_runtime.h>
 
 #include "mq_internal.h"
@@ -63,10 +64,49 @@ __global__ void hop_probe_kernel(const uint64_t *chain, uint32_t hops, uint64_t 
   stamps[kProbeHops + 1] = p;  // the chain's end, so the loads are kept
 }
 
+// Each wave issues `iters` rounds of four independent bf16 MFMAs
+// (v_mfma_f32_32x32x16_bf16) on register operands, two waves per SIMD as the
+// grouped GEMM runs; the sums go to `sink` so the MFMAs are kept.
+typedef __bf16 bf16x8p_t __attribute__((ext_vector_type(8)));
+typedef float f32x16p_t __attribute__((ext_vector_type(16)));
+constexpr uint32_t kMfmaProbeThreads = 512;
+
+__global__ __launch_bounds__(kMfmaProbeThreads, 1) void mfma_probe_kernel(uint32_t iters, float *__restrict__ sink) {
+  bf16x8p_t a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = static_cast<__bf16>(0.001f * static_cast<float>(threadIdx.x + i));
+    b[i] = static_cast<__bf16>(0.002f * static_cast<float>(i));
+  }
+  f32x16p_t acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
+  for (uint32_t it = 0; it < iters; ++it)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc[t], 0, 0, 0);
+  float s = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s += acc[t][r];
+  sink[static_cast<uint64_t>(blockIdx.x) * kMfmaProbeThreads + threadIdx.x] = s;
+}
+
 }  // namespace
 }  // namespace mq
 
 using namespace mq;
+
+extern "C" int mq_mfma_probe(uint32_t iters, uint32_t blocks, float *sink, void *stream) {
+  if (sink == nullptr) return fail(MQ_ERR_INVALID, "sink is required");
+  if (iters == 0 || iters > (1u << 24)) return fail(MQ_ERR_INVALID, "iters must be in 1..2^24");
+  if (blocks == 0 || blocks > 65535u) return fail(MQ_ERR_INVALID, "blocks must be in 1..65535");
+  hipLaunchKernelGGL(mfma_probe_kernel, dim3(blocks), dim3(kMfmaProbeThreads), 0, static_cast<hipStream_t>(stream),
+                     iters, sink);
+  return check_launch("mfma_probe_kernel");
+}
 
 extern "C" int mq_stream_probe(const uint64_t *segments, uint32_t n, uint64_t bytes_each, uint32_t blocks,
                                uint32_t *sink, void *stream) {

@@ -34,7 +34,7 @@ EXPORTS = (
     "mq_available", "mq_init", "mq_last_error", "mq_check_device_errors", "mq_version",
     "mq_abi_struct_size", "mq_record_layout",
     "mq_q4_unpack", "mq_q4_dequant", "mq_q4_qmv", "mq_gather_qmv",
-    "mq_swiglu", "mq_sigmoid", "mq_bf16_round_check", "mq_stream_probe", "mq_hop_probe",
+    "mq_swiglu", "mq_sigmoid", "mq_bf16_round_check", "mq_stream_probe", "mq_hop_probe", "mq_mfma_probe",
     "mq_route_topk", "mq_moe_decode", "mq_moe_layer", "mq_grouped_workspace_size",
     "mq_moe_grouped", "mq_moe_grouped_static", "mq_gather_qmm_workspace_size", "mq_gather_qmm",
     "mq_pool_refill_async", "mq_pool_refill_gather_async",
@@ -201,6 +201,7 @@ def _declare(lib) -> None:
         "mq_pool_refill_gather_async": ([vp, u64, u64, u32, vp, vp, u32, u64, vp, vp], i32),
         "mq_stream_probe": ([vp, u32, u64, u32, vp, vp], i32),
         "mq_hop_probe": ([vp, u32, vp, u32, vp], i32),
+        "mq_mfma_probe": ([u32, u32, vp, vp], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)

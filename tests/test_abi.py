@@ -98,6 +98,9 @@ def test_validation_errors_without_device():
     assert lib.mq_hop_probe(dummy, 9, dummy, 0, None) == _lib.MQ_ERR_INVALID
     assert lib.mq_hop_probe(None, 4, dummy, 0, None) == _lib.MQ_ERR_INVALID
     assert lib.mq_hop_probe(dummy, 4, dummy, 64, None) == _lib.MQ_ERR_INVALID
+    assert lib.mq_mfma_probe(100, 256, None, None) == _lib.MQ_ERR_INVALID
+    assert lib.mq_mfma_probe(0, 256, dummy, None) == _lib.MQ_ERR_INVALID
+    assert lib.mq_mfma_probe(100, 0, dummy, None) == _lib.MQ_ERR_INVALID
 
 
 def test_missing_library_fails_loudly(tmp_path):
