@@ -869,6 +869,9 @@ def main() -> int:
     if not args.no_prefill:
         log("timing the 4096-token prefill grouped path")
         prefill = prefill_bench(torch, dev)
+        peaks = extras.get("peaks_measured")
+        if peaks:  # the same rate against what the matrix cores sustain on this box
+            prefill["mfma_frac_of_issue_rate"] = round(prefill["tflops"] / peaks["bf16_mfma_issue_tflops"], 4)
         log(f"prefill: {prefill}")
     cpu = None
     if not args.no_cpu:
