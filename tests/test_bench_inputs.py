@@ -25,3 +25,26 @@ def test_expert_stage_traffic_parses():
 
 def test_missing_profile_gives_none():
     assert _bench().load_traffic("no_such_kernel") is None
+
+
+def test_more_than_one_gpu_is_refused_before_any_device_work():
+    import subprocess
+    import sys
+
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2
+    assert "one GPU only" in r.stderr
+    assert r.stdout == ""  # no benchmark line
+
+
+def test_zipf_routes_are_distinct_seeded_and_skewed():
+    import numpy as np
+
+    b = _bench()
+    inds = b.zipf_routes(512, 64, 10, seed=3)
+    assert inds.shape == (512, 10) and inds.dtype == np.int32
+    assert all(len(set(row)) == 10 for row in inds.tolist())  # top-k without replacement
+    assert np.array_equal(inds, b.zipf_routes(512, 64, 10, seed=3))
+    counts = np.bincount(inds.reshape(-1), minlength=64)
+    assert counts.max() <= 512 and counts[0] > counts[-1]  # the head expert is the hottest
