@@ -693,11 +693,34 @@ def peaks_bench(torch, dev) -> dict:
     end.record()
     torch.cuda.synchronize()
     mfma_tflops = 2.0 * 32 * 32 * 16 * 4 * iters * 8 * blocks / (start.elapsed_time(end) * 1e-3) / 1e12
+    del sink
+    # Sustained HBM read rate: mq_stream_probe over 2 GiB in 64 segments with
+    # 32 blocks of 256 threads each (about eight blocks per CU), and with one
+    # block per CU, the grouped GEMMs' occupancy.
+    total, n_seg = 2 << 30, 64
+    each = total // n_seg
+    src = torch.ones(total, dtype=torch.uint8, device=dev)
+    segs = torch.tensor([src.data_ptr() + i * each for i in range(n_seg)], dtype=torch.int64, device=dev)
+    word = torch.zeros(1, dtype=torch.int32, device=dev)
+    read_tbps = {}
+    for grid in (2048, 256):
+        for _ in range(2):
+            _lib.check(lib.mq_stream_probe(segs.data_ptr(), n_seg, each, grid, word.data_ptr(), stream), lib)
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(5):
+            _lib.check(lib.mq_stream_probe(segs.data_ptr(), n_seg, each, grid, word.data_ptr(), stream), lib)
+        end.record()
+        torch.cuda.synchronize()
+        read_tbps[grid] = total * 5 / (start.elapsed_time(end) * 1e-3) / 1e12
+    del src, segs
     return {"copy_gbps": round(copy_gbps, 1), "h2d_pinned_gbps": round(h2d_gbps, 1),
             "bf16_gemm_tflops_8192": round(tflops, 1), "bf16_mfma_issue_tflops": round(mfma_tflops, 1),
+            "hbm_read_tbps": round(read_tbps[2048], 2), "hbm_read_tbps_one_block_per_cu": round(read_tbps[256], 2),
             "note": "device-to-device copy counts read + write bytes; host-to-device from 256 MiB of pinned "
                     "memory; GEMM through torch.matmul (hipBLASLt); MFMA issue rate from mq_mfma_probe "
-                    "(256 blocks x 8 waves x 80,000 independent v_mfma_f32_32x32x16_bf16 each)"}
+                    "(256 blocks x 8 waves x 80,000 independent v_mfma_f32_32x32x16_bf16 each); HBM read rate "
+                    "from mq_stream_probe over 2 GiB (2048 blocks of 256 threads, then 256)"}
 
 
 def load_traffic(kernel_tag: str):
@@ -746,6 +769,7 @@ def main() -> int:
     ap.add_argument("--verify-only", action="store_true", help="time only the 4- and 16-token verify layers")
     ap.add_argument("--hotpool-only", action="store_true", help="time only the 6 GB hot-pool stack")
     ap.add_argument("--floors-only", action="store_true", help="time only the decode latency floors")
+    ap.add_argument("--peaks-only", action="store_true", help="time only the measured ceilings")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the expert-parallel "
@@ -764,6 +788,9 @@ def main() -> int:
     torch.cuda.set_device(dev)
     if args.prefill_only:
         print(json.dumps({"prefill": prefill_bench(torch, dev)}), flush=True)
+        return 0
+    if args.peaks_only:
+        print(json.dumps({"peaks_measured": peaks_bench(torch, dev)}), flush=True)
         return 0
     L = args.layers
     log(f"building {L} layers of {EXPERTS} experts (~{L * EXPERTS * expert_bytes_per_record() / 1e9:.1f} GB pool)")
