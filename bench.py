@@ -738,6 +738,38 @@ def load_traffic(kernel_tag: str):
     return None
 
 
+def kernel_rooflines(expert_bytes: int, router_bytes: int):
+    """Per-kernel rooflines of the decode layer from the committed rocprofv3
+    kernel trace (average duration per launch inside 48-layer graph replays,
+    which includes the dispatch gap to the previous kernel): each kernel's
+    algorithmic bytes over its duration, against the 8 TB/s peak."""
+    path = ROOT / "profiles" / "decode_layer_kernel_stats.md"
+    if not path.exists():
+        return None
+    avg = {}
+    for line in path.read_text().splitlines():
+        cells = [c.strip().strip("`") for c in line.split("|")[1:-1]]
+        if len(cells) == 5 and cells[0].endswith((">", "_kernel")):
+            try:
+                avg[cells[0]] = float(cells[2])
+            except ValueError:
+                pass
+    gateup_bytes = expert_bytes * 2 // 3  # gate + up parts of each record (two of its three projections)
+    rows = [("gateup_kernel, routes given", "gateup_kernel<mq::BF16T, 64, 1, 2, false>", gateup_bytes),
+            ("gateup_kernel, selection folded in", "gateup_kernel<mq::BF16T, 64, 1, 2, true>", gateup_bytes),
+            ("down_combine_kernel", "down_combine_kernel<mq::BF16T, 16, 1, 3, 2>", expert_bytes - gateup_bytes),
+            ("router_logits_kernel", "router_logits_kernel", router_bytes)]
+    out = []
+    for label, name, nbytes in rows:
+        us = avg.get(name)
+        if us:
+            gbps = nbytes / (us * 1e-6) / 1e9
+            out.append({"kernel": label, "bytes": nbytes, "profiled_us": us, "achieved": round(gbps, 1),
+                        "frac": round(gbps / HBM_PEAK_GBPS, 4)})
+    return {"source": "profiles/decode_layer_kernel_stats.md", "unit": "GB/s", "peak": HBM_PEAK_GBPS,
+            "kernels": out} if out else None
+
+
 def pmc_pass(torch, runners, stream, handle, copy_mb: int = 256) -> None:
     """Eager launches for `rocprofv3 --pmc`: a plain device copy of known size
     (the counter calibration) and the expert stage of every layer."""
@@ -933,7 +965,8 @@ def main() -> int:
                      "kernel": "expert stage of the layer (gateup_kernel + down_combine_kernel, 11 experts)",
                      "achieved": round(exp_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(exp_gbps / HBM_PEAK_GBPS, 4), "traffic": load_traffic("decode_expert_stage"),
-                     "algorithmic_bytes_per_launch": expert_bytes, "us_per_launch": round(exp_ms * 1000, 3)},
+                     "algorithmic_bytes_per_launch": expert_bytes, "us_per_launch": round(exp_ms * 1000, 3),
+                     "per_kernel": kernel_rooflines(expert_bytes, router_bytes)},
         "prefill": prefill,
         **extras,
         "cpu_baseline": cpu,

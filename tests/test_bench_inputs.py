@@ -48,3 +48,12 @@ def test_zipf_routes_are_distinct_seeded_and_skewed():
     assert np.array_equal(inds, b.zipf_routes(512, 64, 10, seed=3))
     counts = np.bincount(inds.reshape(-1), minlength=64)
     assert counts.max() <= 512 and counts[0] > counts[-1]  # the head expert is the hottest
+
+
+def test_per_kernel_rooflines_parse_from_the_kernel_trace():
+    r = _bench().kernel_rooflines(11 * 1_966_080, 512 * 2048 * 2)
+    assert r is not None
+    names = [k["kernel"] for k in r["kernels"]]
+    assert "down_combine_kernel" in names and "gateup_kernel, routes given" in names
+    for k in r["kernels"]:
+        assert k["profiled_us"] > 0 and 0 < k["frac"] < 1
