@@ -372,12 +372,23 @@ def verify_bench(torch, dev, runners, stream, tokens: int, reps: int = 10) -> di
     time_graph(torch, g, 2, stream)
     ms = time_graph(torch, g, reps, stream) / (reps * len(rs))
     nbytes = (sum(unique) / len(unique) + 1) * expert_bytes_per_record()
-    del g, rs
+    # Check (untimed): every token row of layer 0, as the graph left it, is
+    # bit-identical to the same token through a one-token layer.
+    one = DecodeLayer(runners[0].w, 1, TOP_K, device=dev)
+    same = 0
+    with torch.cuda.stream(stream):
+        for t in range(tokens):
+            one.x.copy_(rs[0].x[t:t + 1])
+            one.launch(handle)
+            torch.cuda.synchronize()
+            same += int(torch.equal(one.out.view(torch.int16), rs[0].out[t:t + 1].view(torch.int16)))
+    del g, rs, one
     return {"tokens": tokens, "path": "mq_moe_layer",
             "us_per_layer": round(ms * 1000, 3), "us_per_token": round(ms * 1000 / tokens, 3),
             "unique_experts_mean": round(sum(unique) / len(unique), 2), "expert_bytes_per_layer": int(nbytes),
             "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4)}
+            "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+            "check": {"rows_bit_identical_to_one_token_layers": same, "rows": tokens}}
 
 
 def stack_bench(torch, dev, runners, stream, steps: int = 128) -> dict:
@@ -412,12 +423,21 @@ def stack_bench(torch, dev, runners, stream, steps: int = 128) -> dict:
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / steps
     nbytes = L * (TOP_K + 1) * expert_bytes_per_record()
-    del g, rs
+    # Check (untimed): the last step's outputs from the graph equal an eager
+    # run of the same step, layer by layer, bit for bit.
+    graph_out = [v.out.clone() for v in rs]
+    with torch.cuda.stream(stream):
+        for v in rs:
+            v.launch(handle)
+    torch.cuda.synchronize()
+    same = sum(int(torch.equal(a.view(torch.int16), v.out.view(torch.int16))) for a, v in zip(graph_out, rs))
+    del g, rs, graph_out
     return {"workload": f"{L} stacked MoE blocks, {steps} decode steps, fresh N(0,1) hidden per step and layer, "
                         f"{L * EXPERTS} expert records in the HBM pool",
             "us_per_token": round(ms * 1000, 2), "expert_bytes_per_token": nbytes,
             "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1), "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-            "router_bytes_per_token": L * EXPERTS * HIDDEN * 2}
+            "router_bytes_per_token": L * EXPERTS * HIDDEN * 2,
+            "check": {"layers_bit_identical_to_eager": same, "layers": L}}
 
 
 def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_steps: int = 2,
