@@ -67,4 +67,4 @@ def make_layout(hidden: int, inter: int, group_size: int = 32) -> SlabLayout:
 
 CHECKPOINT_G32 = make_layout(2560, 640, 32)
 CHECKPOINT_G64 = make_layout(2560, 640, 64)
-BASELINE_G32 = make_layout(2048, 512, 32)
+H2048_I512_G32 = make_layout(2048, 512, 32)

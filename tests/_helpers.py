@@ -11,8 +11,9 @@ import numpy as np
 
 from oracle import bf16, q4
 
-# Value tolerance for bf16 layer outputs (max rel err <= 1e-2
-# and cosine >= 0.9999; the reference's own tests use rtol 2e-2 / atol 3e-3).
+# Value tolerance for bf16 layer outputs (the parity bar of this path: max rel
+# err <= 1e-2 and cosine >= 0.9999; the reference's own tests use rtol 2e-2 /
+# atol 3e-3).
 RTOL = 1e-2
 ATOL = 3e-3
 # The reference's own elementwise tolerance for bf16 executor outputs
