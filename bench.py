@@ -445,9 +445,9 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
     """The 48-block stack decoded through a 6 GB LRU hot pool: per layer the
     router runs, its experts are assigned slots on the host (hits move to the
     LRU tail, misses evict the head), missed records are copied from pinned
-    host memory on a copy stream (`method`: one gather kernel per layer, or one
-    hipMemcpyAsync per record over `copy_engines` streams), and the expert kernels read the pool through
-    slot words.  One host synchronisation per layer (the route hand-off), as in
+    host memory (`method`: one gather kernel per layer on the compute stream,
+    or one hipMemcpyAsync per record over `copy_engines` copy streams), and
+    the expert kernels read the pool through slot words.  One host synchronisation per layer (the route hand-off), as in
     the reference's pool pass.  Host images are the 512 records of layer 0,
     shared by every layer (same bytes per copy as distinct images)."""
     import numpy as np
@@ -480,7 +480,11 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
     gen = torch.Generator(device=dev)
     gen.manual_seed(6)
     xs = torch.randn((warm_steps + steps, L, 1, HIDDEN), generator=gen, device=dev).to(torch.bfloat16)
-    copy_streams = [torch.cuda.Stream() for _ in range(copy_engines)]
+    # The gather kernel runs on the compute stream: the layer's experts wait
+    # for it either way, and a side stream would add two cross-stream event
+    # waits per layer (11-16 us of host time each, measured) while the GPU
+    # idles.  One hipMemcpyAsync per record spreads over the copy engines.
+    copies = [torch.cuda.Stream() for _ in range(copy_engines)] if method == "memcpy" else None
     # Pinned staging for the route words, so that their upload queues behind
     # the refill on the compute stream instead of waiting for it on the host.
     routes_host = [torch.empty(dl.routes.shape, dtype=dl.routes.dtype, pin_memory=True) for dl in dls]
@@ -492,7 +496,7 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
             dl.launch_router(handle)
             inds = dl.inds.cpu()  # the route hand-off (synchronises the stream)
             slots, misses = pool.assign(l, sorted(set(inds.reshape(-1).tolist())))
-            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copy_streams, method=method)
+            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copies, method=method)
             routes_host[l].copy_(HipExpertPool.route_words(slots, inds).view(dl.routes.shape))
             dl.routes.copy_(routes_host[l], non_blocking=True)
             dl.launch_experts(handle)
@@ -529,7 +533,7 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
             dl.launch_router(handle)
             inds = dl.inds.cpu()
             slots, misses = pool.assign(l, sorted(set(inds.reshape(-1).tolist())))
-            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copy_streams, method=method)
+            pool.fill(l, misses, store, compute_stream=stream, copy_stream=copies, method=method)
             dl.routes.copy_(HipExpertPool.route_words(slots, inds).to(dev, non_blocking=False))
             dl.launch_experts(handle)
             torch.cuda.synchronize()
@@ -541,7 +545,8 @@ def hotpool_bench(torch, dev, layers, runners, stream, steps: int = 16, warm_ste
     miss_bytes = misses * stride
     out = {"workload": f"{L} stacked MoE blocks through a {pool_gb:g} GB LRU hot pool ({pool.slots} slots), "
                        f"{steps} decode steps, fresh N(0,1) hidden per step and layer, misses copied from pinned "
-                       + ("host memory by one gather kernel per layer (PCIe reads of the mapped records)"
+                       + ("host memory by one gather kernel per layer on the compute stream (PCIe reads of the "
+                          "mapped records)"
                           if method == "gather" else
                           f"host memory by one hipMemcpyAsync per record on {copy_engines} copy streams"),
            "refill": method,

@@ -85,6 +85,12 @@ class HipExpertPool:
         self.hits = 0
         self.misses = 0
         self._lib = _lib.load()
+        # Events of the fills, created once per stream: `ready` marks the
+        # compute stream's position for the copy streams, `done` each copy
+        # stream's completion.  The first record of a torch event creates the
+        # HIP event (about 12 us on the host), so new events per fill cost more
+        # host time than the refill launch itself.
+        self._events: dict = {}
 
     def _claim_slot(self) -> int:
         """A never-used slot (lowest first) while any is left, else the slot of
@@ -140,7 +146,10 @@ class HipExpertPool:
         of streams: the misses are split into contiguous shares, one per
         stream, so that several DMA engines move them at once.  Returns the
         completion events (one per copy stream used) as a list when
-        ``copy_stream`` is a sequence, else the single event.
+        ``copy_stream`` is a sequence, else the single event.  The events
+        belong to the pool and are recorded again by its next fill on the same
+        copy stream.  With no copy stream (or the compute stream itself) the
+        copies are simply queued on the compute stream.
         """
         if method not in ("gather", "memcpy"):
             raise ValueError(f"method must be 'gather' or 'memcpy', got {method!r}")
@@ -153,13 +162,18 @@ class HipExpertPool:
         misses = list(misses)
         recs = [store.record(layer, e) for e, _slot in misses]  # owned by the store: outlive the copies
         share = -(-len(misses) // len(copies)) if misses else 0
+        ready = None
         events = []
         for i, copy in enumerate(copies):
             part = misses[i * share:(i + 1) * share]
             part_recs = recs[i * share:(i + 1) * share]
-            done = torch.cuda.Event()
-            if copy is not compute:
-                copy.wait_stream(compute)
+            side = copy.cuda_stream != compute.cuda_stream
+            if side:  # the copies start after everything queued on the compute stream
+                if ready is None:
+                    ready = self._event(("ready", compute.cuda_stream))
+                    ready.record(compute)
+                copy.wait_event(ready)
+            done = self._event(("done", copy.cuda_stream))
             n = len(part)
             slots = (ctypes.c_uint32 * max(n, 1))(*[int(slot) for _e, slot in part])
             ptrs = (ctypes.c_void_p * max(n, 1))(*[r.data_ptr() for r in part_recs])
@@ -168,9 +182,15 @@ class HipExpertPool:
             _lib.check(rc, self._lib)
             done.record(copy)
             events.append(done)
-        for done in events:
-            compute.wait_event(done)
+            if side:
+                compute.wait_event(done)
         return events if isinstance(copy_stream, (list, tuple)) else events[0]
+
+    def _event(self, key) -> torch.cuda.Event:
+        ev = self._events.get(key)
+        if ev is None:
+            ev = self._events[key] = torch.cuda.Event()
+        return ev
 
     # ------------------------------------------------------------ addressing
     def projection(self, name: str) -> _lib.MqProjection:
