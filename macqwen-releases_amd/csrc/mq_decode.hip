@@ -241,7 +241,6 @@ __global__ __launch_bounds__(kThreads) void gather_qmv_kernel(
     const typename TT::storage *__restrict__ x, int slot_input, MqProjection proj,
     const uint32_t *__restrict__ routes, typename TT::storage *__restrict__ out, uint32_t pairs, uint32_t slots,
     uint32_t in_w, uint32_t out_w, uint32_t group, uint32_t dense_count, unsigned int *__restrict__ err) {
-  using S = typename TT::storage;
   using Sl = Slice<SW>;
   constexpr int kTileRows = R * Sl::kRows;
   const int lane = threadIdx.x & 63;

@@ -81,15 +81,10 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
                                          __builtin_bit_cast(bf16x2_t, b), acc, false);
 }
 
-// Nibbles k and k+4 of word w (k = 0..3) as the bf16 pair (128+q_k, 128+q_{k+4}).
-// 0x4300 is bf16 128.0 whose 7 mantissa bits count in units of 1.
-template <int K>
-__device__ __forceinline__ uint32_t nib_pair(uint32_t w) {
-  return ((w >> (4 * K)) & 0x000f000fu) | 0x43004300u;
-}
-
-// Activation chunk of 32 inputs held as 16 bf16 pairs matching nib_pair order:
-// for word j (inputs 8j..8j+7): p[4j+k] = (x[8j+k], x[8j+k+4]).
+// Activation chunk of 32 inputs held as 16 bf16 pairs in the order of the
+// weights' nibble pairs (nibbles k and k+4 of a packed word, as the bf16 pair
+// (128+q_k, 128+q_{k+4}); 0x4300 is bf16 128.0, whose 7 mantissa bits count
+// in units of 1): for word j (inputs 8j..8j+7), p[4j+k] = (x[8j+k], x[8j+k+4]).
 struct XChunk {
   uint32_t p[16];
   float osum;  // sum of the 32 bf16 values held in p (removes the 128 offset)
@@ -102,30 +97,6 @@ __device__ __forceinline__ void pairs_from_words(const uint32_t u[4], uint32_t *
   p[1] = __builtin_amdgcn_perm(u[2], u[0], 0x07060302u);  // (x1, x5)
   p[2] = __builtin_amdgcn_perm(u[3], u[1], 0x05040100u);  // (x2, x6)
   p[3] = __builtin_amdgcn_perm(u[3], u[1], 0x07060302u);  // (x3, x7)
-}
-
-// Dot of one packed Q4 chunk (4 words = 32 nibbles) with an activation chunk:
-// returns sum_i x_i * q_i using the 128-offset pairs (the offset is removed
-// with the chunk sum).
-__device__ __forceinline__ float q4_chunk_dot(const uint4 &w, const XChunk &x) {
-  float d = 0.0f;
-  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    d = dot2_bf16(x.p[4 * j + 0], nib_pair<0>(ws[j]), d);
-    d = dot2_bf16(x.p[4 * j + 1], nib_pair<1>(ws[j]), d);
-    d = dot2_bf16(x.p[4 * j + 2], nib_pair<2>(ws[j]), d);
-    d = dot2_bf16(x.p[4 * j + 3], nib_pair<3>(ws[j]), d);
-  }
-  return d - 128.0f * x.osum;
-}
-
-// Sum of the 16 pairs (32 bf16 values) of a chunk.
-__device__ __forceinline__ float chunk_pair_sum(const XChunk &x) {
-  float s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) s = dot2_bf16(x.p[i], 0x3f803f80u, s);
-  return s;
 }
 
 // ---------------------------------------------------------------- DPP reductions
@@ -177,35 +148,14 @@ __device__ __forceinline__ double readlane_d(double v, int lane) {
   return __builtin_bit_cast(double, (hi << 32) | lo);
 }
 
-// Wave-uniform float64 max and sum (all 64 lanes active).  The sum order is
-// fixed: quads, then rows of 16, then the four rows.
-__device__ __forceinline__ double wave_max_f64_uniform(double v) {
-  v = fmax(v, dpp_d<0xb1>(v));
-  v = fmax(v, dpp_d<0x4e>(v));
-  v = fmax(v, dpp_d<0x124>(v));
-  v = fmax(v, dpp_d<0x128>(v));
-  return fmax(fmax(readlane_d(v, 0), readlane_d(v, 16)), fmax(readlane_d(v, 32), readlane_d(v, 48)));
-}
-
+// Wave-uniform float64 sum (all 64 lanes active).  The order is fixed:
+// quads, then rows of 16, then the four rows.
 __device__ __forceinline__ double wave_sum_f64_uniform(double v) {
   v += dpp_d<0xb1>(v);
   v += dpp_d<0x4e>(v);
   v += dpp_d<0x124>(v);
   v += dpp_d<0x128>(v);
   return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
-}
-
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-  for (int off = 32; off > 0; off >>= 1) {
-    uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), off, 64));
-    v = o > v ? o : v;
-  }
-  return v;
 }
 
 // ---------------------------------------------------------------- expert addressing
