@@ -296,12 +296,18 @@ struct SelectOutputs {  // global outputs of the selection (written by block 0)
 // the router selection itself (one wave per token, from the logits) and keeps
 // the route words in LDS; block 0 also publishes the selection.
 template <class TT, int SW, int CPL, int R, bool SELECT>
+// The arguments are ordered for the kernel-argument preload (14 dwords): first
+// what the selection and the activation loads need at the start, then the rest.
 __global__ __launch_bounds__(kThreads) void gateup_kernel(
-    const typename TT::storage *__restrict__ x, MqProjection gate, MqProjection up, SharedExpert shared,
-    bool has_shared, const uint32_t *__restrict__ routes, const int32_t *__restrict__ keeps, SelectParams sel,
+    const uint16_t *__restrict__ sel_logits, const uint32_t *__restrict__ sel_slot_table,
+    const typename TT::storage *__restrict__ x, uint32_t sel_experts, uint32_t sel_top_k, uint32_t tokens,
+    uint32_t slots, uint32_t tile_limit, uint32_t has_shared_u, uint32_t hidden, uint32_t inter,
+    uint32_t sel_min_keep, float sel_threshold, float sel_blend, MqProjection gate, MqProjection up,
+    SharedExpert shared, const uint32_t *__restrict__ routes, const int32_t *__restrict__ keeps,
     SelectOutputs sel_out, typename TT::storage *__restrict__ act, typename TT::storage *__restrict__ gate_out,
-    typename TT::storage *__restrict__ up_out, uint32_t tokens, uint32_t slots, uint32_t hidden, uint32_t inter,
-    uint32_t group, uint32_t dense_count, uint32_t tile_limit, unsigned int *__restrict__ err) {
+    typename TT::storage *__restrict__ up_out, uint32_t group, uint32_t dense_count, unsigned int *__restrict__ err) {
+  const SelectParams sel{sel_logits, sel_slot_table, sel_experts, sel_top_k, sel_min_keep, sel_threshold, sel_blend};
+  const bool has_shared = has_shared_u != 0u;
   using Sl = Slice<SW>;
   constexpr int kTileRows = R * Sl::kRows;
   __shared__ RouteLds lds;
@@ -448,13 +454,15 @@ enum SharedMode : int { kSharedNone = 0, kSharedY = 1, kSharedParts = 2, kShared
 // (metal_runtime.py:908-929).  Padded slots (s >= keep) carry score 0 and are
 // skipped.
 template <class TT, int SW, int CPL, int SPW, int R>
+// The arguments are ordered for the kernel-argument preload: first the inputs
+// of the first round of loads (route words, scores, keep count, activations).
 __global__ __launch_bounds__(kThreads) void down_combine_kernel(
-    const typename TT::storage *__restrict__ act, MqProjection down, SharedExpert shared,
-    const uint32_t *__restrict__ routes, const void *__restrict__ scores, int score_dtype,
-    const int32_t *__restrict__ keeps, int shared_mode, const typename TT::storage *__restrict__ shared_vec,
-    const uint16_t *__restrict__ shared_gate, typename TT::storage *__restrict__ out, uint32_t tokens,
-    uint32_t slots, uint32_t hidden, uint32_t inter, uint32_t group, uint32_t dense_count, bool generic,
-    unsigned int *__restrict__ err) {
+    const uint32_t *__restrict__ routes, const void *__restrict__ scores, const int32_t *__restrict__ keeps,
+    const typename TT::storage *__restrict__ act, const uint16_t *__restrict__ shared_gate, int score_dtype,
+    int shared_mode, uint32_t tokens, uint32_t slots, uint32_t inter, MqProjection down, SharedExpert shared,
+    const typename TT::storage *__restrict__ shared_vec, typename TT::storage *__restrict__ out, uint32_t hidden,
+    uint32_t group, uint32_t dense_count, uint32_t generic_u, unsigned int *__restrict__ err) {
+  const bool generic = generic_u != 0u;
   using Sl = Slice<SW>;
   constexpr uint32_t kMaxSources = kMaxSlots + 1;
   constexpr uint32_t kBlockRows = Sl::kRows * R;  // R row groups of kRows rows
@@ -690,9 +698,10 @@ void launch_gateup_r(const MqMoeArgs &a, const SharedExpert &shared, bool has_sh
   constexpr int kTileRows = R * Slice<SW>::kRows;
   const uint32_t tiles = pairs * ceil_div(a.inter, kTileRows);
   hipLaunchKernelGGL((gateup_kernel<TT, SW, CPL, R, SELECT>), dim3(ceil_div(tiles, kWaves)), dim3(kThreads), 0,
-                     stream, static_cast<const S *>(a.x), a.gate, a.up, shared, has_shared, a.routes, keeps, sel,
-                     sel_out, act, static_cast<S *>(a.gate_out), static_cast<S *>(a.up_out), a.tokens, a.slots,
-                     a.hidden, a.inter, a.group_size, a.expert_count, tiles, err);
+                     stream, sel.logits, sel.slot_table, static_cast<const S *>(a.x), sel.experts, sel.top_k,
+                     a.tokens, a.slots, tiles, has_shared ? 1u : 0u, a.hidden, a.inter, sel.min_keep, sel.threshold,
+                     sel.blend, a.gate, a.up, shared, a.routes, keeps, sel_out, act, static_cast<S *>(a.gate_out),
+                     static_cast<S *>(a.up_out), a.group_size, a.expert_count, err);
 }
 
 // Gate/up launch.  With 64-lane slices a wave takes 2, 4 or 8 rows per tile:
@@ -730,10 +739,10 @@ void launch_down_r(const MqMoeArgs &a, const SharedExpert &shared, int shared_mo
                    unsigned int *err, hipStream_t stream) {
   using S = typename TT::storage;
   const dim3 grid(ceil_div(a.hidden, Slice<SW>::kRows * R), a.tokens);
-  hipLaunchKernelGGL((down_combine_kernel<TT, SW, CPL, SPW, R>), grid, dim3(kThreads), 0, stream, act, a.down, shared,
-                     a.routes, a.scores, a.score_dtype, keeps, shared_mode, shared_vec, a.shared_gate,
-                     static_cast<S *>(a.out), a.tokens, a.slots, a.hidden, a.inter, a.group_size, a.expert_count,
-                     a.group_size == 64 || (a.flags & MQ_DECODE_GENERIC_COMBINE) != 0, err);
+  hipLaunchKernelGGL((down_combine_kernel<TT, SW, CPL, SPW, R>), grid, dim3(kThreads), 0, stream, a.routes, a.scores,
+                     keeps, act, a.shared_gate, a.score_dtype, shared_mode, a.tokens, a.slots, a.inter, a.down, shared,
+                     shared_vec, static_cast<S *>(a.out), a.hidden, a.group_size, a.expert_count,
+                     (a.group_size == 64 || (a.flags & MQ_DECODE_GENERIC_COMBINE) != 0) ? 1u : 0u, err);
 }
 
 template <class TT, int SW, int CPL, int SPW, int R>
@@ -898,9 +907,10 @@ int moe_decode_t(const MqMoeArgs &a, hipStream_t stream, const MqRouteArgs *rout
         constexpr int kTileRows = R * Slice<SW>::kRows;
         const uint32_t tiles = a.tokens * ceil_div(a.inter, kTileRows);
         hipLaunchKernelGGL((gateup_kernel<TT, SW, CPL, R, false>), dim3(ceil_div(tiles, kWaves)), dim3(kThreads), 0,
-                           stream, static_cast<const S *>(a.x), a.gate, a.up, shared, true, a.routes, keeps,
-                           SelectParams{}, SelectOutputs{}, act, nullptr, nullptr, a.tokens, a.slots, a.hidden,
-                           a.inter, a.group_size, ne, tiles, err);
+                           stream, static_cast<const uint16_t *>(nullptr), static_cast<const uint32_t *>(nullptr),
+                           static_cast<const S *>(a.x), 0u, 0u, a.tokens, a.slots, tiles, 1u, a.hidden, a.inter, 0u,
+                           0.0f, 0.0f, a.gate, a.up, shared, a.routes, keeps, SelectOutputs{}, act,
+                           static_cast<S *>(nullptr), static_cast<S *>(nullptr), a.group_size, ne, err);
       });
       if ((rc = check_launch("gateup_kernel"))) return rc;
     }
