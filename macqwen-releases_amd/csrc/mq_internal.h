@@ -148,6 +148,15 @@ __device__ __forceinline__ double readlane_d(double v, int lane) {
   return __builtin_bit_cast(double, (hi << 32) | lo);
 }
 
+// Wave-uniform max of unsigned keys (all 64 lanes active).
+__device__ __forceinline__ uint32_t wave_max_u32_uniform(uint32_t v) {
+  v = max(v, dpp_u<0xb1>(v));
+  v = max(v, dpp_u<0x4e>(v));
+  v = max(v, dpp_u<0x124>(v));
+  v = max(v, dpp_u<0x128>(v));
+  return max(max(readlane_u(v, 0), readlane_u(v, 16)), max(readlane_u(v, 32), readlane_u(v, 48)));
+}
+
 // Wave-uniform float64 sum (all 64 lanes active).  The order is fixed:
 // quads, then rows of 16, then the four rows.
 __device__ __forceinline__ double wave_sum_f64_uniform(double v) {

@@ -253,65 +253,21 @@ __device__ __forceinline__ void sort8_desc(uint32_t (&key)[kSelMaxPerLane]) {
   }
 }
 
-// Merges the partner's two largest keys (pa > pb, or zeros) into this lane's
-// (a > b): the pair stays the two largest of the union.  The sets merged are
-// always disjoint, so no key is counted twice.
-__device__ __forceinline__ void top2_merge(uint32_t &a, uint32_t &b, uint32_t pa, uint32_t pb) {
-  const uint32_t lo = min(a, pa);
-  a = max(a, pa);
-  b = max(lo, max(b, pb));
-}
-
-// The two largest keys of the wave, in every lane, from each lane's two
-// largest (a > b).  Rows of 16 lanes merge through DPP (quad swaps, then
-// rotations by 4 and 8 lanes); the four rows then merge through the gfx950
-// lane swaps (lanes 32-63 against 0-31, then 16-31 against 0-15 in each
-// half), so the result never passes through scalar registers.
-__device__ __forceinline__ void wave_top2_u32(uint32_t &a, uint32_t &b) {
-  top2_merge(a, b, dpp_u<0xb1>(a), dpp_u<0xb1>(b));    // quad_perm [1,0,3,2]
-  top2_merge(a, b, dpp_u<0x4e>(a), dpp_u<0x4e>(b));    // quad_perm [2,3,0,1]
-  top2_merge(a, b, dpp_u<0x124>(a), dpp_u<0x124>(b));  // row_ror:4
-  top2_merge(a, b, dpp_u<0x128>(a), dpp_u<0x128>(b));  // row_ror:8
-  // Each swap returns the two halves' values side by side; merging the two
-  // results combines disjoint halves whichever way round they come.
-  const auto a32 = __builtin_amdgcn_permlane32_swap(a, a, false, false);
-  const auto b32 = __builtin_amdgcn_permlane32_swap(b, b, false, false);
-  a = a32[0];
-  b = b32[0];
-  top2_merge(a, b, a32[1], b32[1]);
-  const auto a16 = __builtin_amdgcn_permlane16_swap(a, a, false, false);
-  const auto b16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
-  a = a16[0];
-  b = b16[0];
-  top2_merge(a, b, a16[1], b16[1]);
-}
-
-// Top-k over unique keys.  Each lane sorts its keys; each round takes the two
-// largest remaining keys of the wave (from the lanes' two heads) and the lanes
-// holding them pop them (one lane may pop both).  Lane j keeps the j-th
-// selected key (descending); other lanes get 0.  `key` is consumed.
+// Top-k over unique keys.  Each lane sorts its keys; round j takes the wave
+// max of the lanes' heads and the winning lane pops its head.  Lane j keeps
+// the j-th selected key (descending); other lanes get 0.  `key` is consumed.
 __device__ __forceinline__ uint32_t select_keys(uint32_t (&key)[kSelMaxPerLane], uint32_t k, int lane) {
   sort8_desc(key);
   uint32_t mine = 0u;
 #pragma unroll
-  for (uint32_t j = 0; j < static_cast<uint32_t>(kSelMaxTopK); j += 2) {
+  for (uint32_t j = 0; j < static_cast<uint32_t>(kSelMaxTopK); ++j) {
     if (j < k) {  // wave-uniform
-      uint32_t m1 = key[0], m2 = key[1];
-      wave_top2_u32(m1, m2);
-      const bool two = j + 1u < k;  // wave-uniform
-      mine = static_cast<uint32_t>(lane) == j ? m1 : mine;
-      if (two) mine = static_cast<uint32_t>(lane) == j + 1u ? m2 : mine;
-      // The second key sits at the head of its lane or right behind the
-      // first (then key[0] == m1).  Past the last nonzero key, m2 == 0 and
-      // the lanes that match it shift zeros.
-      const bool p1 = key[0] == m1;
-      const bool p2 = two && (key[0] == m2 || key[1] == m2);
+      const uint32_t best = wave_max_u32_uniform(key[0]);
+      mine = static_cast<uint32_t>(lane) == j ? best : mine;
+      const bool win = key[0] == best;
 #pragma unroll
-      for (int i = 0; i < kSelMaxPerLane; ++i) {
-        const uint32_t k1 = i + 1 < kSelMaxPerLane ? key[i + 1] : 0u;
-        const uint32_t k2 = i + 2 < kSelMaxPerLane ? key[i + 2] : 0u;
-        key[i] = p1 && p2 ? k2 : (p1 || p2) ? k1 : key[i];
-      }
+      for (int i = 0; i < kSelMaxPerLane - 1; ++i) key[i] = win ? key[i + 1] : key[i];
+      key[kSelMaxPerLane - 1] = win ? 0u : key[kSelMaxPerLane - 1];
     }
   }
   return mine;
